@@ -1,0 +1,262 @@
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline: the 4-bit group-32 decode GEMV, weights N=6144 x K=2048
+int4x (opentpu/quant.py int4: nibbles + per-row Sw, per-block dw, per-32 multipliers m, from
+N(0, 0.02)), one int8 MX activation row from N(0, 1).  A step is one launch of B independent
+such GEMVs (B weight sets resident in HBM, > 512 MB in total, so no step is served from the
+256 MB Infinity Cache); value = algorithmic bytes moved per second (GB/s, 1e9).
+
+The same JSON line carries the other configs' figures under "extra": c1 int8 GEMV, c5 LM head
++ greedy argmax, c3 prefill GEMM (int8 TOPS), each timed with HIP events on the stream the
+kernels run on; and the CPU baseline (the C oracle, OpenMP, on this host) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, vendor figure
+INT8_PEAK_TOPS = 5000.0          # MI355X dense int8 MFMA, vendor figure
+
+
+def c2_bytes(N=6144, K=2048):
+    """Algorithmic bytes of one 4-bit GEMV: elements N*K/2, scale rows 72 B/row, activation
+    K int8 + K/32 offsets + Sa, output 4 B/row."""
+    return N * K // 2 + N * (8 + 8 * ((K // 128 + 1) // 2)) + K + K // 32 + 4 + 4 * N
+
+
+def c1_bytes(N=4096, K=1024):
+    return N * K + 4 * N + K + K // 32 + 4 + 4 * N
+
+
+def c5_bytes(N=262144, K=2560):
+    return N * K + 4 * N + K + K // 32 + 4 + 4 * N
+
+
+def timed(fn, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps          # ms per step
+
+
+def make_batch(fmt, B, N, K, seed, rsc=False):
+    """B independent weight sets and activation rows, generated and packed on the GPU."""
+    import torch
+
+    from opentpu_amd import fp32, quant
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    rows = srows = None
+    for b in range(B):
+        W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+        r, s = quant.quantize_mxu(W, fmt, rsc=rsc)
+        if rows is None:
+            rows = torch.empty((B,) + tuple(r.shape), dtype=torch.uint8, device="cuda")
+            srows = torch.empty((B,) + tuple(s.shape), dtype=torch.uint8, device="cuda")
+        rows[b].copy_(r)
+        srows[b].copy_(s)
+        del W, r, s
+    x = torch.randn((B, K), generator=gen, device="cuda")
+    q, Sa, da = fp32.quantize_mx(x, 32)
+    return rows, srows, q, Sa, da
+
+
+def batched_gemv(fmt, B, N, K, seed, steps, warmup, rsc=False):
+    import torch
+
+    from opentpu_amd import _lib as X
+    rows, srows, q, Sa, da = make_batch(fmt, B, N, K, seed, rsc)
+    out = torch.empty((B, N), dtype=torch.float32, device="cuda")
+    rs, srs = rows.shape[2], srows.shape[2]
+    fl = X.RSC if rsc else 0
+    st = X.stream()
+
+    def step():
+        X.call("otpu_mm_batched", B, X.ptr(q), K, K, X.ptr(Sa), 1, X.ptr(da), K // 32, K // 32, 1, K,
+               X.ptr(rows), rs, N * rs, X.ptr(srows), srs, N * srs, N, X.FMT[fmt], fl, 0, X.ptr(out), N, N, st)
+    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    single = rows[0], srows[0], q[:1], Sa[:1], da[:1]
+    return ms, single
+
+
+def single_gemv_ms(fmt, single, N, K, steps, rsc=False):
+    """One GEMV per launch, cycling over weight copies held by the batch (not cache-resident)."""
+    import torch
+
+    from opentpu_amd import _lib as X
+    rows, srows, q, Sa, da = single
+    out = torch.empty((1, N), dtype=torch.float32, device="cuda")
+    st = X.stream()
+
+    def step():
+        X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, 1, K, X.ptr(rows), rows.shape[1],
+               X.ptr(srows), srows.shape[1], N, X.FMT[fmt], X.RSC if rsc else 0, 0, None, X.ptr(out), N, None, st)
+    return timed(step, steps, 3, torch.cuda.current_stream())
+
+
+def lm_head(steps, warmup):
+    import torch
+
+    from opentpu_amd import _lib as X
+    from opentpu_amd import fp32, quant
+    N, K = 262144, 2560
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+    rows, srows = quant.quantize_mxu(W, "int8", rsc=True)
+    del W
+    x = torch.randn((1, K), generator=gen, device="cuda")
+    q, Sa, da = fp32.quantize_mx(x, 32)
+    logits = torch.empty((N,), dtype=torch.float32, device="cuda")
+    best = torch.empty((1,), dtype=torch.int64, device="cuda")
+    tok = torch.empty((1,), dtype=torch.int32, device="cuda")
+    st = X.stream()
+
+    def step():
+        X.call("otpu_lm_head_argmax", X.ptr(q), X.ptr(Sa), X.ptr(da), K, X.ptr(rows), K, X.ptr(srows), 4, N,
+               X.FMT["int8"], X.RSC, 0, 0, X.ptr(logits), X.ptr(best), X.ptr(tok), st)
+    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    return ms, int(tok.item())
+
+
+def gemm(steps, warmup):
+    import torch
+
+    from opentpu_amd import _lib as X
+    from opentpu_amd import fp32, quant
+    M, K, N = 512, 2048, 8192
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+    rows, srows = quant.quantize_mxu(W, "int8", rsc=True)
+    x = torch.randn((M, K), generator=gen, device="cuda")
+    q, Sa, da = fp32.quantize_mx(x, 32, row_mode=True)
+    out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    st = X.stream()
+
+    def step():
+        X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, M, K, X.ptr(rows), K, X.ptr(srows), 4, N,
+               X.FMT["int8"], X.RSC, 0, None, X.ptr(out), N, None, st)
+    return timed(step, steps, warmup, torch.cuda.current_stream())
+
+
+def cpu_baseline(seconds=10.0):
+    """The C oracle (OpenMP) on this host: one c2 GEMV repeated for about `seconds`."""
+    from oracle import cpu as OC
+    from oracle import formats as Q
+    from oracle import fp32 as F
+    threads = min(16, os.cpu_count() or 1)
+    OC.threads(threads)
+    rng = np.random.default_rng(2)
+    N, K = 6144, 2048
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    rows, srows = Q.pack_x4(W, "int4")
+    q, Sa, da = F.quantize_mx(rng.standard_normal((1, K)).astype(np.float32), 32)
+    t0 = time.perf_counter()
+    OC.mm(q, Sa, da, rows, srows, "int4", K)
+    one = time.perf_counter() - t0
+    reps = max(1, min(2000, int(seconds / max(one, 1e-4))))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        OC.mm(q, Sa, da, rows, srows, "int4", K)
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": round(c2_bytes() / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"c2 int4 GEMV 6144x2048, {reps} calls of the C oracle (oracle/cpu_mm.c, OpenMP), "
+                      f"{dt * 1e3:.2f} ms per call"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=80)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c5 (default: all)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3", "c5"}
+    extra = {}
+
+    N2, K2, B2 = 6144, 2048, args.batch
+    ms2, single2 = batched_gemv("int4", B2, N2, K2, 2, args.steps, args.warmup)
+    gbs2 = B2 * c2_bytes() / (ms2 * 1e-3) / 1e9
+    print(f"[c2] batched int4 GEMV: {ms2:.4f} ms/step, {gbs2:.1f} GB/s", file=sys.stderr, flush=True)
+    ms2s = single_gemv_ms("int4", single2, N2, K2, 200)
+    extra["c2_single_launch"] = {"us": round(ms2s * 1e3, 3), "GBps": round(c2_bytes() / (ms2s * 1e-3) / 1e9, 1)}
+    del single2
+    torch.cuda.empty_cache()
+
+    if "c1" in only:
+        B1 = 128
+        ms1, s1 = batched_gemv("int8", B1, 4096, 1024, 1, 20, 3, rsc=True)
+        extra["c1_int8_rsc_gemv"] = {"batch": B1, "ms": round(ms1, 4),
+                                     "GBps": round(B1 * c1_bytes() / (ms1 * 1e-3) / 1e9, 1)}
+        ms1s = single_gemv_ms("int8", s1, 4096, 1024, 200, rsc=True)
+        extra["c1_single_launch"] = {"us": round(ms1s * 1e3, 3)}
+        del s1
+        torch.cuda.empty_cache()
+        print(f"[c1] {extra['c1_int8_rsc_gemv']}", file=sys.stderr, flush=True)
+    if "c5" in only:
+        ms5, tok = lm_head(10, 2)
+        extra["c5_lm_head_argmax"] = {"us": round(ms5 * 1e3, 2), "token": tok,
+                                      "GBps": round(c5_bytes() / (ms5 * 1e-3) / 1e9, 1),
+                                      "frac_hbm": round(c5_bytes() / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        torch.cuda.empty_cache()
+        print(f"[c5] {extra['c5_lm_head_argmax']}", file=sys.stderr, flush=True)
+    if "c3" in only:
+        ms3 = gemm(5, 1)
+        tops = 2 * 512 * 2048 * 8192 / (ms3 * 1e-3) / 1e12
+        extra["c3_gemm_row_x_rsc"] = {"us": round(ms3 * 1e3, 2), "TOPS": round(tops, 2),
+                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        print(f"[c3] {extra['c3_gemm_row_x_rsc']}", file=sys.stderr, flush=True)
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": "quant GEMV GB/s (% HBM peak) + prefill int8 GEMM TOPS, 1 MI355X",
+        "value": round(gbs2, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms2, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,0.02) weights packed on the GPU, N(0,1) activations)",
+        "config": {"workload": f"c2: 4-bit int4x group-32 decode GEMV N={N2} K={K2}, {B2} independent "
+                               f"weight sets per launch", "batch": B2, "N": N2, "K": K2, "fmt": "int4"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs2, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs2 / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,122 @@
+/* opentpu_amd: the C ABI of the MI355X quantized-linear hot path (openTPU's MM, QACT and
+ * greedy ARGMAX as HIP kernels for gfx950).
+ *
+ * Conventions
+ *   - Every pointer is device memory owned by the caller (hipMalloc or a torch tensor's
+ *     data_ptr()); sizes and strides are in elements of the pointed-to type unless the name
+ *     says bytes (`rs`, `srs` are bytes, like the reference's).
+ *   - Every call is asynchronous on `stream` (a hipStream_t; NULL = the null stream) and
+ *     allocates nothing.
+ *   - Return value: OTPU_OK (0) or a negative OTPU_E* code; the message of the last failure
+ *     on the calling thread is otpu_last_error().  The argument checks mirror the reference
+ *     simulator's SimError checks (opentpu/isasim.py:767-822).
+ *   - Layouts are the reference's byte for byte, so packed weights from
+ *     opentpu/quant.py:quantize_mxu load unchanged (opentpu/quant.py:287-449, docs/isa.md:277-304).
+ */
+#ifndef OTPU_H
+#define OTPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* otpu_stream_t; /* hipStream_t */
+
+enum {
+    OTPU_OK = 0,
+    OTPU_EINVAL = -1,   /* a shape, stride or field out of range */
+    OTPU_EALIGN = -2,   /* a pointer or stride not aligned as the kernels need */
+    OTPU_EFORMAT = -3,  /* an unknown weight format or a format / flag combination refused */
+    OTPU_ELAUNCH = -4,  /* a HIP launch error */
+    OTPU_ENODEV = -5    /* no usable gfx950 device */
+};
+
+/* Weight formats (opentpu/isa.py:26-28: W8, W4I, W4F, WNV; shift windows 16, 11, 11, 13). */
+enum { OTPU_INT8 = 0, OTPU_INT4 = 1, OTPU_FP4 = 2, OTPU_NVFP4 = 3 };
+
+/* MM flags, the reference's bits (opentpu/isa.py:21, :29-30). PAIR changes no result bit
+ * (a scheduling mode of the MXU) and is accepted and ignored. */
+enum {
+    OTPU_UNIT = 0x1,
+    OTPU_ACC = 0x2,
+    OTPU_RMAX = 0x4,
+    OTPU_ASCALE = 0x8,
+    OTPU_PAIR = 0x40,
+    OTPU_RSC = 0x80
+};
+
+const char* otpu_last_error(void);
+int otpu_version(void);
+
+/* QACT's quantizer: fp32.quantize_mx(x, g, row_mode) of M rows of K
+ * (opentpu/fp32.py:321-343; the instruction: opentpu/isasim.py:913-959, opentpu/isa.py:551).
+ *   x [M, ldx] fp32 -> q [M, ldq] int8, S [M] fp32 (amax * f32(1/127)), d [M, ldd] uint8
+ *   (K/g power-of-two group offsets; all 0 with row_mode).  g in {8, 16, 32, 64, 128}
+ *   (QACT: 32 = D/4; QST and the int8x weight packer: 128 = D), K a multiple of g and of 4. */
+int otpu_qact(const float* x, int M, int K, int64_t ldx, int g, int row_mode, int8_t* q,
+              int64_t ldq, float* S, uint8_t* d, int64_t ldd, otpu_stream_t stream);
+
+/* MM (opentpu/isasim.py:749-910, opentpu/isa.py:502; semantics docs/isa.md:226-305), natural
+ * row layout, rows of one:
+ *   q [M, ldq] int8, Sa [M], da [M, ldda] uint8 (an offset per 32 of K): the operand one QACT
+ *   range wrote; w: N weight rows `rs` bytes apart (int8: K bytes; 4-bit: K/2 bytes, element
+ *   2i in the low nibble); ws: N scale rows `srs` bytes apart (ignored with UNIT); the MM's
+ *   block k uses the scale rows' block k0 + k.  out [M, ors] fp32:
+ *     out[j, n] = (i2f(acc) * Sw[n]) * (Sa[j] * 2^-W)   (then ACC / ASCALE as the flags say)
+ *   with acc the exact integer sum over 32-groups of (m << (W - dw - da)) * c (dropped where
+ *   the shift is negative).  alpha [M] (ASCALE only), rowmax [M] (RMAX only; may be NULL
+ *   otherwise).  K a multiple of 128; w, rs multiples of 16 bytes; ws, srs multiples of 4. */
+int otpu_mm(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda,
+            int M, int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N,
+            int fmt, int flags, int k0, const float* alpha, float* out, int64_t ors,
+            float* rowmax, otpu_stream_t stream);
+
+/* The same MM's exact accumulators acc [M, N] (int64), no epilogue (parity and debugging:
+ * the int64 row sums of opentpu/isasim.py:879-898). */
+int otpu_mm_acc(const int8_t* q, int64_t ldq, const uint8_t* da, int64_t ldda, int M, int K,
+                const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt,
+                int flags, int k0, int64_t* acc, otpu_stream_t stream);
+
+/* B independent MMs of one shape in one launch (a layer stack's or an expert set's decode
+ * GEMVs): problem b's operands start at the given pointers plus b times the *_bstride
+ * (elements of each pointer's type; bytes for w and ws).  No ACC / ASCALE / RMAX. */
+int otpu_mm_batched(int B, const int8_t* q, int64_t ldq, int64_t q_bstride, const float* Sa,
+                    int64_t sa_bstride, const uint8_t* da, int64_t ldda, int64_t da_bstride,
+                    int M, int K, const uint8_t* w, int64_t rs, int64_t w_bstride,
+                    const uint8_t* ws, int64_t srs, int64_t ws_bstride, int N, int fmt,
+                    int flags, int k0, float* out, int64_t ors, int64_t out_bstride,
+                    otpu_stream_t stream);
+
+/* LM head + greedy: one activation row (M = 1) times N vocabulary rows, the logits' total-order
+ * maximum with the first index (opentpu/llm/qwen3.py:2052-2088 + opentpu/llm/generate.py:251-286
+ * + VOP ARGMAX opentpu/isasim.py:1141-1152).  best = max over n of (key(y_n) << 32 | ~(base+n))
+ * (a u64 whose low word is the complement of the index); token = base + that n.  logits may be
+ * NULL. */
+int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8_t* da, int K,
+                        const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N,
+                        int fmt, int flags, int k0, int64_t base, float* logits,
+                        uint64_t* best, int32_t* token, otpu_stream_t stream);
+
+/* VOP ARGMAX (opentpu/isasim.py:1141-1152, opentpu/isa.py:633): per row of x [rows, ldx] the
+ * (maximum, i2f(first column + base)) fp32 pair into pairs[r * drs + 0..1]. */
+int otpu_argmax(const float* x, int rows, int cols, int64_t ldx, int64_t base, float* pairs,
+                int64_t drs, otpu_stream_t stream);
+
+/* Weight packers, bit-exact with opentpu/quant.py:quantize_mxu (no counterpart kernel in the
+ * reference: it packs on the host in numpy).
+ *   otpu_pack_int8: int8x (quant.py:316-322, rsc = 0; scale rows of 4 + 4*ceil(KB/4) bytes) or
+ *   RSC rows (runtime.py:66-76 with row=True, rsc = 1; scale rows of 4 bytes).
+ *   otpu_pack_x4: int4x / fp4x6 (quant.py:325-367; fmt OTPU_INT4 or OTPU_FP4): element rows of
+ *   ceil(K/256)*128 bytes, scale rows of 8 + 8*ceil(KB/2) bytes. */
+int otpu_pack_int8(const float* W, int N, int K, int64_t ldw, int rsc, uint8_t* rows,
+                   int64_t rs, uint8_t* srows, int64_t srs, otpu_stream_t stream);
+int otpu_pack_x4(const float* W, int N, int K, int64_t ldw, int fmt, uint8_t* rows, int64_t rs,
+                 uint8_t* srows, int64_t srs, otpu_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OTPU_H */

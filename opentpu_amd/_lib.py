@@ -1,0 +1,125 @@
+"""ctypes binding of libotpu_amd.so (the C ABI of include/otpu.h) and the torch plumbing the
+Python API uses: device tensors, their pointers and the current HIP stream.
+
+There is no CPU fallback: every operation runs the HIP kernels, and loading fails loudly when
+the library is not built or no GPU is present."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libotpu_amd.so")
+
+INT8, INT4, FP4, NVFP4 = 0, 1, 2, 3
+FMT = {"int8": INT8, "int4": INT4, "fp4": FP4, "nvfp4": NVFP4}
+UNIT, ACC, RMAX, ASCALE, PAIR, RSC = 0x1, 0x2, 0x4, 0x8, 0x40, 0x80
+
+# every exported symbol and its argument types (P pointer, L int64, I int32)
+_P, _L, _I = C.c_void_p, C.c_int64, C.c_int
+SIGNATURES = {
+    "otpu_last_error": ([], C.c_char_p),
+    "otpu_version": ([], _I),
+    "otpu_qact": ([_P, _I, _I, _L, _I, _I, _P, _L, _P, _P, _L, _P], _I),
+    "otpu_mm": ([_P, _L, _P, _P, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P, _P], _I),
+    "otpu_mm_acc": ([_P, _L, _P, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P], _I),
+    "otpu_mm_batched": ([_I, _P, _L, _L, _P, _L, _P, _L, _L, _I, _I, _P, _L, _L, _P, _L, _L, _I, _I, _I,
+                         _I, _P, _L, _L, _P], _I),
+    "otpu_lm_head_argmax": ([_P, _P, _P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _L, _P, _P, _P, _P], _I),
+    "otpu_argmax": ([_P, _I, _I, _L, _L, _P, _L, _P], _I),
+    "otpu_pack_int8": ([_P, _I, _I, _L, _I, _P, _L, _P, _L, _P], _I),
+    "otpu_pack_x4": ([_P, _I, _I, _L, _I, _P, _L, _P, _L, _P], _I),
+}
+
+
+class OtpuError(RuntimeError):
+    """A call the C ABI refused (the reference raises SimError for the same checks)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """The library, with argument types set (no GPU needed to load it)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built: run `python -m opentpu_amd.build` "
+                               "(there is no CPU fallback)")
+        lib = C.CDLL(path)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        raise OtpuError(rc, load().otpu_last_error().decode())
+
+
+def torch():
+    import torch as T
+    if not T.cuda.is_available():
+        raise RuntimeError("opentpu_amd needs a GPU (HIP device); none is visible")
+    return T
+
+
+def stream():
+    """The current torch stream of the current device, as a hipStream_t."""
+    return C.c_void_p(torch().cuda.current_stream().cuda_stream)
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+_NP2T = {np.float32: "float32", np.int8: "int8", np.uint8: "uint8", np.int64: "int64",
+         np.int32: "int32", np.uint64: "uint64"}
+
+
+def dev(x, dtype):
+    """A contiguous device tensor of dtype (a numpy dtype) from a numpy array or a tensor."""
+    T = torch()
+    tdt = getattr(T, _NP2T[np.dtype(dtype).type])
+    if isinstance(x, T.Tensor):
+        if x.dtype != tdt:
+            if tdt == T.uint8 and x.dtype == T.int8 or tdt == T.int8 and x.dtype == T.uint8:
+                x = x.view(tdt)
+            else:
+                x = x.to(tdt)
+        return x.cuda().contiguous()
+    a = np.ascontiguousarray(x)
+    if a.dtype != np.dtype(dtype):
+        if a.dtype.itemsize == np.dtype(dtype).itemsize and a.dtype.kind in "iu" and np.dtype(dtype).kind in "iu":
+            a = a.view(dtype)
+        else:
+            a = a.astype(dtype)
+    return T.from_numpy(a).cuda()
+
+
+def empty(shape, dtype):
+    T = torch()
+    return T.empty(shape, dtype=getattr(T, _NP2T[np.dtype(dtype).type]), device="cuda")
+
+
+def zeros(shape, dtype):
+    T = torch()
+    return T.zeros(shape, dtype=getattr(T, _NP2T[np.dtype(dtype).type]), device="cuda")
+
+
+def is_numpy(x) -> bool:
+    return isinstance(x, np.ndarray) or np.isscalar(x)
+
+
+def host(t):
+    return t.cpu().numpy()

@@ -1,0 +1,514 @@
+// MM for few activation rows (decode GEMV, M <= 4 per launch): the weight-streaming kernel,
+// the LM head with the greedy argmax fused into its epilogue, and VOP ARGMAX.
+// Semantics: opentpu/isasim.py:706-910 (MM), :1141-1152 (ARGMAX), docs/isa.md:226-305.
+//
+// Layout of the work.  A weight row is cut into 16-byte pieces (int8: 16 elements, half a
+// 32-group; 4-bit: 32 elements, one 32-group).  A wave owns R weight rows at a time and lane l
+// takes pieces l, l+64, l+128, .. of each (L = ceil(pieces/64) per lane), so every load is a
+// 16-byte global_load_dwordx4 and a wave's load covers 1 KB of one row.  The activation pieces
+// a lane needs are the same for every row: they are loaded once, into registers (4-bit: split
+// into even / odd element bytes to meet the nibbles).  Per piece:
+//   int8   c = 4 x v_dot4_i32_i8
+//   int4   c = 8 x v_dot4 on (nibble << 4) bytes, then >> 4 (exact)
+//   fp4    E2M1 codes through two v_perm_b32 tables and a sign select, then 8 x v_dot4
+// then B = m << (W - dw - da) (0 where the shift is negative) and an int64 multiply-add.  The
+// wave reduces each row's int64 partials with shuffles and R*M lanes run the fp32 epilogue
+// (three FTZ products) and store.  Scale rows are read per lane piece (4 lanes share a word).
+#include "otpu_common.h"
+
+namespace otpu {
+
+constexpr int LMAX = 8;            // pieces per lane held in registers (K <= 128 * LMAX * 16 / elements)
+
+struct MMArgs {
+    const int8_t* q; int64_t ldq;
+    const float* Sa;
+    const uint8_t* da; int64_t ldda;
+    int M, K;
+    const uint8_t* w; int64_t rs;
+    const uint8_t* ws; int64_t srs;
+    int N, flags, k0;
+    const float* alpha;
+    float* out; int64_t ors;
+    uint32_t* rmax_key;            // RMAX: total-order keys, finished by rmax_finish
+    int64_t* acc_out;              // exact accumulators instead of the epilogue
+    uint64_t* best;                // LM head: max of (key << 32 | ~index)
+    int64_t base;                  // LM head: index of row 0
+    int P, T;                      // 16-byte pieces per row, lanes per row (team)
+    // batch strides (elements of each pointer's type; bytes for w / ws)
+    int64_t q_bs, sa_bs, da_bs, w_bs, ws_bs, out_bs;
+};
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// a streamed 16-byte weight load, marked non-temporal (the rows are read once)
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) {
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// E2M1 codes (4 per dword, one per byte, 0..15) -> signed int8 values, twice the E2M1 value
+__device__ __forceinline__ uint32_t dec_e2m1(uint32_t nib) {
+    uint32_t sel = nib & 0x07070707u;
+    uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel);
+    uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, sel);
+    uint32_t msk = ((nib >> 3) & 0x01010101u) * 0xFFu;
+    return (neg & msk) | (pos & ~msk);
+}
+
+// piece sums: int8 (one partial 16-group of a 32-group), 4-bit (c0: whole 32-group, or with
+// nvfp4 the two 16-groups c0 and c1)
+template <int FMT>
+__device__ __forceinline__ void piece_dot(const uint4 wv, const uint32_t* a, int& c0, int& c1) {
+    if (FMT == OTPU_INT8) {
+        int c = __builtin_amdgcn_sdot4((int)wv.x, (int)a[0], 0, false);
+        c = __builtin_amdgcn_sdot4((int)wv.y, (int)a[1], c, false);
+        c = __builtin_amdgcn_sdot4((int)wv.z, (int)a[2], c, false);
+        c0 = __builtin_amdgcn_sdot4((int)wv.w, (int)a[3], c, false);
+        c1 = 0;
+    } else if (FMT == OTPU_INT4) {
+        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        int c = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            c = __builtin_amdgcn_sdot4((int)((wd[t] << 4) & 0xF0F0F0F0u), (int)a[2 * t], c, false);
+            c = __builtin_amdgcn_sdot4((int)(wd[t] & 0xF0F0F0F0u), (int)a[2 * t + 1], c, false);
+        }
+        c0 = c >> 4;
+        c1 = 0;
+    } else {
+        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        int c[2] = {0, 0};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t ev = dec_e2m1(wd[t] & 0x0F0F0F0Fu), od = dec_e2m1((wd[t] >> 4) & 0x0F0F0F0Fu);
+            c[t >> 1] = __builtin_amdgcn_sdot4((int)ev, (int)a[2 * t], c[t >> 1], false);
+            c[t >> 1] = __builtin_amdgcn_sdot4((int)od, (int)a[2 * t + 1], c[t >> 1], false);
+        }
+        if (FMT == OTPU_NVFP4) { c0 = c[0]; c1 = c[1]; }
+        else { c0 = c[0] + c[1]; c1 = 0; }
+    }
+}
+
+// the scale data a piece of row `srow` needs (UNIT / RSC: none)
+template <int FMT>
+__device__ __forceinline__ uint32_t piece_scale(const uint8_t* srow, int k0, int p, bool plain) {
+    if (plain) return 0;
+    if (FMT == OTPU_INT8) return srow[4 + k0 + (p >> 3)];
+    if (FMT == OTPU_NVFP4)
+        return *reinterpret_cast<const uint16_t*>(srow + 16 + 8 * (k0 + (p >> 2)) + 2 * (p & 3));
+    return *reinterpret_cast<const uint32_t*>(srow + 8 + 4 * (k0 + (p >> 2)));
+}
+
+// B * c for the piece's group(s); shA = W - da of the piece's 32-group (activation side)
+template <int FMT>
+__device__ __forceinline__ int64_t piece_term(int c0, int c1, uint32_t sc, int shA, int p, bool plain) {
+    if (FMT == OTPU_INT8) {
+        int sh = shA - (plain ? 0 : (int)sc);
+        return sh >= 0 ? ((int64_t)c0 << sh) : 0;
+    }
+    if (FMT == OTPU_NVFP4) {
+        int64_t t = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            int e4 = (int)((sc >> (8 * h)) & 0xFF), E = (e4 >> 3) & 15, mt = e4 & 7;
+            int m = plain ? 1 : (E ? 8 + mt : mt);
+            int sh = shA - (plain ? 0 : 15 - (E > 1 ? E : 1));
+            t += sh >= 0 ? (int64_t)(m << sh) * (int64_t)(h ? c1 : c0) : 0;
+        }
+        return t;
+    }
+    int m = plain ? 1 : (int)((sc >> (8 + 6 * (p & 3))) & 63);
+    int sh = shA - (plain ? 0 : (int)(sc & 0xFF));
+    return sh >= 0 ? (int64_t)(m << sh) * (int64_t)c0 : 0;
+}
+
+// rows a team takes per iteration: about four 16-byte loads in flight per lane
+template <int L>
+constexpr int rows_per_team() { return L >= 4 ? 1 : (L == 1 ? 4 : 2); }
+
+// activation registers a lane holds: MR rows x L pieces x (4 int8 | 8 split 4-bit) dwords
+template <int FMT, int MR, int L>
+constexpr bool fits() { return MR * L * (FMT == OTPU_INT8 ? 4 : 8) <= 64; }
+
+template <int FMT, int MR, int L>
+__global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
+    constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
+    constexpr int R = rows_per_team<L>();
+    const int lane = threadIdx.x & 63;
+    const int T = a.T, NT = 64 / T;                       // lanes per team, teams per wave
+    const int tl = lane & (T - 1), team = lane / T;
+    const int b = blockIdx.y;                             // batch problem
+    const int8_t* q = a.q + b * a.q_bs;
+    const float* Sa = a.Sa ? a.Sa + b * a.sa_bs : nullptr;
+    const uint8_t* da = a.da + b * a.da_bs;
+    const uint8_t* w = a.w + b * a.w_bs;
+    const uint8_t* ws = a.ws + b * a.ws_bs;
+    float* out = a.out ? a.out + b * a.out_bs : nullptr;
+    const bool plain = (a.flags & (OTPU_UNIT | OTPU_RSC)) != 0;
+    const bool unit = (a.flags & OTPU_UNIT) != 0;
+    const int W = window_of(FMT);
+    const int P = a.P;
+
+    // activation pieces tl, tl + T, .. and their W - da, per act row, in registers
+    uint32_t act[MR][L][AW];
+    int shA[MR][L];
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+            const int p = i * T + tl;
+            const bool ok = p < P && j < a.M;
+            if (FMT == OTPU_INT8) {
+                uint4 v = ok ? *reinterpret_cast<const uint4*>(q + j * a.ldq + 16 * p) : make_uint4(0, 0, 0, 0);
+                act[j][i][0] = v.x; act[j][i][1] = v.y; act[j][i][2] = v.z; act[j][i][3] = v.w;
+                shA[j][i] = W - (ok ? (int)da[j * a.ldda + (p >> 1)] : 0);
+            } else {
+                uint4 v0 = make_uint4(0, 0, 0, 0), v1 = v0;
+                if (ok) {
+                    v0 = *reinterpret_cast<const uint4*>(q + j * a.ldq + 32 * p);
+                    v1 = *reinterpret_cast<const uint4*>(q + j * a.ldq + 32 * p + 16);
+                }
+                const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    act[j][i][2 * t] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x06040200u);
+                    act[j][i][2 * t + 1] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x07050301u);
+                }
+                shA[j][i] = W - (ok ? (int)da[j * a.ldda + p] : 0);
+            }
+        }
+    }
+    float sa2[MR];
+#pragma unroll
+    for (int j = 0; j < MR; ++j) sa2[j] = (j < a.M && !a.acc_out) ? fmul(Sa[j], pow2f(-W)) : 0.0f;
+
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    const int RW = R * NT;                      // rows a wave takes per iteration
+    uint64_t best = 0;
+    const int er = tl / MR, ej = tl % MR;       // epilogue lane tl = r * MR + j of its team
+
+    for (int n0 = wave * RW; n0 < a.N; n0 += nwaves * RW) {
+        uint4 wv[R][L];
+        uint32_t sc[R][L];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = n0 + r * NT + team;
+            const uint8_t* row = w + (int64_t)n * a.rs;
+            const uint8_t* srow = ws + (int64_t)n * a.srs;
+#pragma unroll
+            for (int i = 0; i < L; ++i) {
+                const int p = i * T + tl;
+                const bool ok = p < P && n < a.N;
+                wv[r][i] = ok ? ld16(row + 16 * p) : make_uint4(0, 0, 0, 0);
+                sc[r][i] = ok ? piece_scale<FMT>(srow, a.k0, p, plain) : 0u;
+            }
+        }
+        const int n = n0 + er * NT + team;     // this lane's epilogue output row
+        const bool epi = tl < R * MR && n < a.N && ej < a.M;
+        float sw = 1.0f;
+        if (epi && !unit) sw = *reinterpret_cast<const float*>(ws + (int64_t)n * a.srs);
+
+        int64_t mine = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int j = 0; j < MR; ++j) {
+                int64_t acc = 0;
+#pragma unroll
+                for (int i = 0; i < L; ++i) {
+                    int c0, c1;
+                    piece_dot<FMT>(wv[r][i], act[j][i], c0, c1);
+                    acc += piece_term<FMT>(c0, c1, sc[r][i], shA[j][i], i * T + tl, plain);
+                }
+                for (int o = T >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+                if (tl == r * MR + j) mine = acc;
+            }
+        }
+        if (epi) {
+            if (a.acc_out) {
+                a.acc_out[(int64_t)ej * a.N + n] = mine;
+            } else {
+                float y = fmul(fmul(i2f(mine), sw), sa2[ej]);
+                if (out) {
+                    float* o = out + (int64_t)ej * a.ors + n;
+                    if (a.flags & OTPU_ASCALE) y = fadd(fmul(*o, a.alpha[ej]), y);
+                    else if (a.flags & OTPU_ACC) y = fadd(*o, y);
+                    *o = y;
+                }
+                if (a.flags & OTPU_RMAX) atomicMax(a.rmax_key + ej, fkey(y));
+                if (a.best) {
+                    uint64_t cand = ((uint64_t)fkey(y) << 32) | (uint32_t)~(uint32_t)(a.base + n);
+                    best = cand > best ? cand : best;
+                }
+            }
+        }
+    }
+    if (a.best) {                               // one atomic per wave
+        best = wave_max_u64(best);
+        if (lane == 0 && best) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)best);
+    }
+}
+
+// a fill kernel (graph-capture friendly, no memset nodes)
+__global__ void fill_u32(uint32_t* p, int n, uint32_t v) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void rmax_finish(uint32_t* k, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) k[i] = fbits(unkey(k[i]));
+}
+
+__global__ void best_finish(const uint64_t* best, int32_t* token) {
+    if (threadIdx.x == 0) *token = (int32_t)~(uint32_t)(*best & 0xFFFFFFFFull);
+}
+
+// VOP ARGMAX: one workgroup per row; (max, i2f(index + base))
+__global__ __launch_bounds__(256) void argmax_rows(const float* __restrict__ x, int cols, int64_t ldx,
+                                                    int64_t base, float* pairs, int64_t drs) {
+    __shared__ uint64_t red[4];
+    const float* xr = x + (int64_t)blockIdx.x * ldx;
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        uint64_t cand = ((uint64_t)fkey(xr[c]) << 32) | (uint32_t)~(uint32_t)c;
+        best = cand > best ? cand : best;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = red[0];
+        for (int i = 1; i < 4; ++i) b = red[i] > b ? red[i] : b;
+        const uint32_t idx = ~(uint32_t)(b & 0xFFFFFFFFu);
+        float* o = pairs + (int64_t)blockIdx.x * drs;
+        o[0] = unkey((uint32_t)(b >> 32));
+        o[1] = i2f((int64_t)(int32_t)(uint32_t)((int64_t)idx + base));
+    }
+}
+
+}  // namespace otpu
+
+using namespace otpu;
+
+static bool al(const void* p, int a) { return ((uintptr_t)p & (uintptr_t)(a - 1)) == 0; }
+
+// the SimError-style checks of one MM (opentpu/isasim.py:767-822, the fields of isa.py:502-548)
+static int check_mm(const char* who, const int8_t* q, int64_t ldq, const uint8_t* da, int64_t ldda,
+                    int M, int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs,
+                    int N, int fmt, int flags, int k0) {
+    if (fmt < OTPU_INT8 || fmt > OTPU_NVFP4) return otpu_fail(OTPU_EFORMAT, "%s: weight format %d", who, fmt);
+    if (M < 1 || N < 1 || K < OTPU_D || K % OTPU_D || k0 < 0)
+        return otpu_fail(OTPU_EINVAL, "%s: M %d, N %d, K %d (a multiple of %d), k0 %d", who, M, N, K, OTPU_D, k0);
+    if ((flags & OTPU_RSC) && fmt == OTPU_NVFP4) return otpu_fail(OTPU_EFORMAT, "%s: RSC does not take NVFP4", who);
+    if ((flags & OTPU_ASCALE) && !((flags & OTPU_UNIT) && (flags & OTPU_ACC)))
+        return otpu_fail(OTPU_EINVAL, "%s: ASCALE needs UNIT and ACC", who);
+    if (flags & ~(OTPU_UNIT | OTPU_ACC | OTPU_RMAX | OTPU_ASCALE | OTPU_PAIR | OTPU_RSC))
+        return otpu_fail(OTPU_EINVAL, "%s: unknown flags %#x", who, flags);
+    const int KB = K / OTPU_D;
+    const int64_t rowb = fmt == OTPU_INT8 ? K : K / 2;
+    if (!q || !da || !w) return otpu_fail(OTPU_EINVAL, "%s: a NULL operand", who);
+    if (ldq < K || ldda < K / 32 || rs < rowb)
+        return otpu_fail(OTPU_EINVAL, "%s: ldq %lld, ldda %lld, rs %lld too small", who, (long long)ldq,
+                         (long long)ldda, (long long)rs);
+    if (!(flags & OTPU_UNIT)) {
+        if (!ws) return otpu_fail(OTPU_EINVAL, "%s: NULL scale rows", who);
+        int64_t need = 4;
+        if (!(flags & OTPU_RSC))
+            need = fmt == OTPU_INT8 ? 4 + k0 + KB : fmt == OTPU_NVFP4 ? 16 + 8 * (k0 + KB) : 8 + 4 * (k0 + KB);
+        const int sal = fmt == OTPU_NVFP4 ? 16 : (fmt == OTPU_INT8 || (flags & OTPU_RSC)) ? 4 : 8;
+        if (srs < need) return otpu_fail(OTPU_EINVAL, "%s: scale rows of %lld bytes, blocks k0 %d + %d need %lld",
+                                         who, (long long)srs, k0, KB, (long long)need);
+        if (!al(ws, 4) || srs % sal)
+            return otpu_fail(OTPU_EALIGN, "%s: ssa and srs must be multiples of %d", who, sal);
+    }
+    if (!al(w, 16) || rs % 16 || !al(q, 16) || ldq % 16)
+        return otpu_fail(OTPU_EALIGN, "%s: weight rows and activations 16-byte aligned (w, rs, q, ldq)", who);
+    if ((rowb / 16 + 63) / 64 > LMAX)
+        return otpu_fail(OTPU_EINVAL, "%s: K %d exceeds the register-resident operand (%d 16-byte pieces a lane)",
+                         who, K, LMAX);
+    return OTPU_OK;
+}
+
+template <int FMT, int MR, int L>
+static void launch_one(const MMArgs& a, int batch, hipStream_t s) {
+    if constexpr (fits<FMT, MR, L>()) {
+        constexpr int R = rows_per_team<L>();
+        const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
+        int64_t blocks = (waves + 3) / 4;
+        const int64_t cap = (int64_t)otpu_cu_count() * 8;
+        if (blocks > cap) blocks = cap;
+        gemv_kernel<FMT, MR, L><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+    }
+}
+
+template <int FMT, int MR>
+static void launch_L(const MMArgs& a, int L, int batch, hipStream_t s) {
+    switch (L) {
+        case 1: launch_one<FMT, MR, 1>(a, batch, s); break;
+        case 2: launch_one<FMT, MR, 2>(a, batch, s); break;
+        case 3: launch_one<FMT, MR, 3>(a, batch, s); break;
+        case 4: launch_one<FMT, MR, 4>(a, batch, s); break;
+        case 5: launch_one<FMT, MR, 5>(a, batch, s); break;
+        case 6: launch_one<FMT, MR, 6>(a, batch, s); break;
+        default: launch_one<FMT, MR, 8>(a, batch, s); break;
+    }
+}
+
+template <int FMT>
+static void launch_fmt(const MMArgs& a, int mr, int L, int batch, hipStream_t s) {
+    if (mr == 1) launch_L<FMT, 1>(a, L, batch, s);
+    else if (mr == 2) launch_L<FMT, 2>(a, L, batch, s);
+    else launch_L<FMT, 4>(a, L, batch, s);
+}
+
+// lanes per row: the team size in {64, 32, 16} that wastes the fewest lane pieces
+static void pick_team(int P, int* T, int* L) {
+    int bt = 64, bl = (P + 63) / 64, bw = bl * 64 - P;
+    for (int t = 32; t >= 16; t >>= 1) {
+        int l = (P + t - 1) / t, w = l * t - P;
+        if (l <= LMAX && w < bw) { bt = t; bl = l; bw = w; }
+    }
+    if (bl == 7) bl = 8;                        // (no L = 7 instantiation: the eighth is masked)
+    *T = bt;
+    *L = bl;
+}
+
+static int mr_max(int fmt, int L) {
+    const int aw = fmt == OTPU_INT8 ? 4 : 8;
+    return 4 * L * aw <= 64 ? 4 : (2 * L * aw <= 64 ? 2 : 1);
+}
+
+static int launch_gemv(MMArgs a, int fmt, int batch, hipStream_t s) {
+    const int64_t rowb = fmt == OTPU_INT8 ? a.K : a.K / 2;
+    a.P = (int)(rowb / 16);
+    int L = 1;
+    pick_team(a.P, &a.T, &L);
+    const int M = a.M, cap = mr_max(fmt, L);
+    for (int j0 = 0; j0 < M; j0 += cap) {        // activation rows in chunks the registers hold
+        MMArgs c = a;
+        c.M = M - j0 < cap ? M - j0 : cap;
+        const int mr = c.M == 1 ? 1 : (c.M == 2 ? 2 : 4);
+        c.q = a.q + j0 * a.ldq;
+        if (a.Sa) c.Sa = a.Sa + j0;
+        c.da = a.da + j0 * a.ldda;
+        if (c.out) c.out = a.out + j0 * a.ors;
+        if (c.alpha) c.alpha = a.alpha + j0;
+        if (c.rmax_key) c.rmax_key = a.rmax_key + j0;
+        if (c.acc_out) c.acc_out = a.acc_out + (int64_t)j0 * a.N;
+        switch (fmt) {
+            case OTPU_INT8: launch_fmt<OTPU_INT8>(c, mr, L, batch, s); break;
+            case OTPU_INT4: launch_fmt<OTPU_INT4>(c, mr, L, batch, s); break;
+            case OTPU_FP4: launch_fmt<OTPU_FP4>(c, mr, L, batch, s); break;
+            default: launch_fmt<OTPU_NVFP4>(c, mr, L, batch, s); break;
+        }
+    }
+    return otpu_launch_check("mm");
+}
+
+static MMArgs make_args(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda, int M,
+                        int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int flags,
+                        int k0) {
+    MMArgs a = {};
+    a.q = q; a.ldq = ldq; a.Sa = Sa; a.da = da; a.ldda = ldda; a.M = M; a.K = K;
+    a.w = w; a.rs = rs; a.ws = ws; a.srs = srs; a.N = N; a.flags = flags & ~OTPU_PAIR; a.k0 = k0;
+    return a;
+}
+
+int otpu_gemm_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda, int M, int K,
+                  const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
+                  float* out, int64_t ors, hipStream_t s);
+
+extern "C" int otpu_mm(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda,
+                       int M, int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N,
+                       int fmt, int flags, int k0, const float* alpha, float* out, int64_t ors,
+                       float* rowmax, otpu_stream_t stream) {
+    int rc = check_mm("mm", q, ldq, da, ldda, M, K, w, rs, ws, srs, N, fmt, flags, k0);
+    if (rc) return rc;
+    if (!Sa || !out || ors < N) return otpu_fail(OTPU_EINVAL, "mm: Sa / out NULL or ors < N");
+    if ((flags & OTPU_ASCALE) && !alpha) return otpu_fail(OTPU_EINVAL, "mm: ASCALE without alpha");
+    if ((flags & OTPU_RMAX) && !rowmax) return otpu_fail(OTPU_EINVAL, "mm: RMAX without rowmax");
+    hipStream_t s = (hipStream_t)stream;
+    if (M > 4 && !(flags & (OTPU_ACC | OTPU_ASCALE | OTPU_RMAX)) && k0 == 0) {
+        rc = otpu_gemm_try(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, fmt, flags, out, ors, s);
+        if (rc <= 0) return rc;                       // handled (or failed); > 0: not this path
+    }
+    MMArgs a = make_args(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, flags, k0);
+    a.alpha = alpha; a.out = out; a.ors = ors;
+    if (flags & OTPU_RMAX) {
+        a.rmax_key = reinterpret_cast<uint32_t*>(rowmax);
+        fill_u32<<<(M + 255) / 256, 256, 0, s>>>(a.rmax_key, M, 0u);
+    }
+    rc = launch_gemv(a, fmt, 1, s);
+    if (rc) return rc;
+    if (flags & OTPU_RMAX) {
+        rmax_finish<<<(M + 255) / 256, 256, 0, s>>>(a.rmax_key, M);
+        return otpu_launch_check("mm rmax");
+    }
+    return OTPU_OK;
+}
+
+extern "C" int otpu_mm_acc(const int8_t* q, int64_t ldq, const uint8_t* da, int64_t ldda, int M, int K,
+                           const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt,
+                           int flags, int k0, int64_t* acc, otpu_stream_t stream) {
+    int rc = check_mm("mm_acc", q, ldq, da, ldda, M, K, w, rs, ws, srs, N, fmt,
+                      flags & ~(OTPU_ACC | OTPU_ASCALE | OTPU_RMAX), k0);
+    if (rc) return rc;
+    if (!acc) return otpu_fail(OTPU_EINVAL, "mm_acc: NULL acc");
+    MMArgs a = make_args(q, ldq, nullptr, da, ldda, M, K, w, rs, ws, srs, N,
+                         flags & ~(OTPU_ACC | OTPU_ASCALE | OTPU_RMAX), k0);
+    a.acc_out = acc;
+    return launch_gemv(a, fmt, 1, (hipStream_t)stream);
+}
+
+extern "C" int otpu_mm_batched(int B, const int8_t* q, int64_t ldq, int64_t q_bstride, const float* Sa,
+                               int64_t sa_bstride, const uint8_t* da, int64_t ldda, int64_t da_bstride, int M,
+                               int K, const uint8_t* w, int64_t rs, int64_t w_bstride, const uint8_t* ws,
+                               int64_t srs, int64_t ws_bstride, int N, int fmt, int flags, int k0, float* out,
+                               int64_t ors, int64_t out_bstride, otpu_stream_t stream) {
+    if (B < 1 || B > 65535) return otpu_fail(OTPU_EINVAL, "mm_batched: B %d", B);
+    if (flags & (OTPU_ACC | OTPU_ASCALE | OTPU_RMAX))
+        return otpu_fail(OTPU_EINVAL, "mm_batched: no ACC, ASCALE or RMAX");
+    int rc = check_mm("mm_batched", q, ldq, da, ldda, M, K, w, rs, ws, srs, N, fmt, flags, k0);
+    if (rc) return rc;
+    if (!Sa || !out || ors < N) return otpu_fail(OTPU_EINVAL, "mm_batched: Sa / out NULL or ors < N");
+    if (q_bstride % 16 || w_bstride % 16 || (!(flags & OTPU_UNIT) && ws_bstride % 4))
+        return otpu_fail(OTPU_EALIGN, "mm_batched: batch strides keep the operands aligned");
+    MMArgs a = make_args(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, flags, k0);
+    a.out = out; a.ors = ors;
+    a.q_bs = q_bstride; a.sa_bs = sa_bstride; a.da_bs = da_bstride;
+    a.w_bs = w_bstride; a.ws_bs = ws_bstride; a.out_bs = out_bstride;
+    return launch_gemv(a, fmt, B, (hipStream_t)stream);
+}
+
+extern "C" int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8_t* da, int K, const uint8_t* w,
+                                   int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
+                                   int64_t base, float* logits, uint64_t* best, int32_t* token,
+                                   otpu_stream_t stream) {
+    if (flags & (OTPU_ACC | OTPU_ASCALE | OTPU_RMAX))
+        return otpu_fail(OTPU_EINVAL, "lm_head_argmax: no ACC, ASCALE or RMAX");
+    int rc = check_mm("lm_head_argmax", q, K, da, K / 32, 1, K, w, rs, ws, srs, N, fmt, flags, k0);
+    if (rc) return rc;
+    if (!Sa || !best || !token) return otpu_fail(OTPU_EINVAL, "lm_head_argmax: NULL Sa, best or token");
+    if (base < 0 || base + (int64_t)N > 0xFFFFFFFFll) return otpu_fail(OTPU_EINVAL, "lm_head_argmax: base %lld", (long long)base);
+    if (!al(best, 8)) return otpu_fail(OTPU_EALIGN, "lm_head_argmax: best 8-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    MMArgs a = make_args(q, K, Sa, da, K / 32, 1, K, w, rs, ws, srs, N, flags, k0);
+    a.out = logits; a.ors = N; a.best = best; a.base = base;
+    fill_u32<<<1, 64, 0, s>>>(reinterpret_cast<uint32_t*>(best), 2, 0u);
+    rc = launch_gemv(a, fmt, 1, s);
+    if (rc) return rc;
+    best_finish<<<1, 64, 0, s>>>(best, token);
+    return otpu_launch_check("lm_head_argmax");
+}
+
+extern "C" int otpu_argmax(const float* x, int rows, int cols, int64_t ldx, int64_t base, float* pairs,
+                           int64_t drs, otpu_stream_t stream) {
+    if (rows < 1 || cols < 1 || ldx < cols || !x || !pairs || (rows > 1 && drs < 2))
+        return otpu_fail(OTPU_EINVAL, "argmax: rows %d, cols %d, ldx %lld, drs %lld", rows, cols,
+                         (long long)ldx, (long long)drs);
+    argmax_rows<<<rows, 256, 0, (hipStream_t)stream>>>(x, cols, ldx, base, pairs, drs);
+    return otpu_launch_check("argmax");
+}

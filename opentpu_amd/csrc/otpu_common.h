@@ -1,0 +1,118 @@
+// Device helpers shared by the HIP kernels: the machine's fp32 arithmetic (IEEE RNE with
+// flush-to-zero on operands and results, canonical NaN), the exact int64 -> fp32 conversion,
+// recip, q8 and the total-order key.  Semantics: opentpu/fp32.py:45-121, :162-172, :242-261
+// and docs/isa.md:88-135 of the reference.  Every file that includes this is compiled with
+// -ffp-contract=off and fp32 denormals enabled, so each `a * b` below is one rounded v_mul_f32
+// on the subnormal grid and the flushes are explicit.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/otpu.h"
+
+#define OTPU_D 128          // K-block (MXU depth)
+
+namespace otpu {
+
+__device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
+__device__ __forceinline__ float bitsf(uint32_t u) { return __uint_as_float(u); }
+
+__device__ __forceinline__ float ftz(float x) {
+    uint32_t u = fbits(x);
+    return ((u & 0x7F800000u) == 0) ? bitsf(u & 0x80000000u) : x;
+}
+// an arithmetic result: flush a denormal, canonical NaN
+__device__ __forceinline__ float fin(float r) {
+    r = ftz(r);
+    return (r != r) ? bitsf(0x7FC00000u) : r;
+}
+__device__ __forceinline__ float fmul(float a, float b) { return fin(ftz(a) * ftz(b)); }
+__device__ __forceinline__ float fadd(float a, float b) { return fin(ftz(a) + ftz(b)); }
+__device__ __forceinline__ float fsub(float a, float b) { return fin(ftz(a) - ftz(b)); }
+__device__ __forceinline__ float pow2f(int d) { return bitsf((uint32_t)(d + 127) << 23); }
+
+// total-order key of flushed bits: the unsigned order of keys is -NaN < -inf < .. < -0 < +0
+// < .. < inf < NaN
+__device__ __forceinline__ uint32_t fkey(float x) {
+    uint32_t u = fbits(ftz(x));
+    return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float unkey(uint32_t k) {
+    return bitsf((k >> 31) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// signed int64 -> fp32, round to nearest even, exact for every input (MM's |acc| < 2^47)
+__device__ __forceinline__ float i2f(int64_t v) {
+    uint64_t u = v < 0 ? (uint64_t)0 - (uint64_t)v : (uint64_t)v;
+    float s;
+    if (u < (1ull << 24)) {
+        s = (float)(uint32_t)u;
+    } else {
+        int sh = 40 - __clzll((long long)u);          // bits below the 24-bit significand
+        uint64_t mant = u >> sh;
+        uint64_t rem = u & ((1ull << sh) - 1);
+        uint64_t half = 1ull << (sh - 1);
+        mant += (rem > half || (rem == half && (mant & 1))) ? 1 : 0;
+        s = ldexpf((float)(uint32_t)mant, sh);         // mant <= 2^24: exact
+    }
+    return v < 0 ? -s : s;
+}
+
+// recip: seed 0x7EF311C3 - bits(a) on the significand a in [1, 2), two Newton steps, the
+// correction step y*e + y, then 127 - exponent field added back; zero -> +0, |x| >= 2^126
+// (and inf / NaN bits) -> a zero with x's sign.
+__device__ __forceinline__ float recip(float x) {
+    x = ftz(x);
+    uint32_t xb = fbits(x), mag = xb & 0x7FFFFFFFu, sign = xb & 0x80000000u;
+    if (mag == 0) return 0.0f;
+    if (mag >= 0x7E800000u) return bitsf(sign);
+    float a = bitsf(0x3F800000u | (mag & 0x7FFFFFu));
+    float y = bitsf(0x7EF311C3u - fbits(a));
+    y = fmul(y, fsub(2.0f, fmul(a, y)));
+    y = fmul(y, fsub(2.0f, fmul(a, y)));
+    y = fadd(fmul(y, fsub(1.0f, fmul(a, y))), y);
+    int32_t k = 127 - (int32_t)(mag >> 23);
+    return bitsf((uint32_t)((int32_t)fbits(y) + k * (1 << 23)) | sign);
+}
+
+// q8: round half to even, saturate to +-127, NaN -> 0
+__device__ __forceinline__ int q8(float x) {
+    x = ftz(x);
+    if (x != x) return 0;
+    float r = __builtin_rintf(x);
+    r = r > 127.0f ? 127.0f : (r < -127.0f ? -127.0f : r);
+    return (int)r;
+}
+
+__device__ __forceinline__ int window_of(int fmt) {
+    return fmt == OTPU_INT8 ? 16 : (fmt == OTPU_NVFP4 ? 13 : 11);
+}
+
+// wave-wide reductions (wave64)
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint64_t w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v, int width) {
+    for (int o = width >> 1; o > 0; o >>= 1) {
+        uint32_t w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+}  // namespace otpu
+
+// host-side error reporting shared by the entry points (abi.hip)
+int otpu_fail(int code, const char* fmt, ...);
+int otpu_launch_check(const char* what);
+int otpu_cu_count();

@@ -1,0 +1,274 @@
+"""GPU parity: the HIP kernels through the C ABI (opentpu_amd) against the CPU oracle on the
+same seeded inputs, bit for bit (int8 operands, int64 accumulators, fp32 outputs, tokens)."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import same_bits
+from oracle import cpu as OC
+from oracle import formats as Q
+from oracle import fp32 as F
+from oracle import mm as MM
+from test_oracle_mm import CASES, mm_case
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "x4_packer.npz")
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ops():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    from opentpu_amd import _lib, fp32, mxu, quant
+    _lib.load()
+    return fp32, quant, mxu
+
+
+def spread(rng, M, K, s=6.0, g=8):
+    return (rng.standard_normal((M, K)) * np.exp(rng.uniform(-s, s, (M, K // g, 1)))
+            .repeat(g, 2).reshape(M, K)).astype(np.float32)
+
+
+@pytest.mark.parametrize("g,row_mode", [(32, False), (32, True), (128, False), (8, False), (64, False)])
+def test_qact(ops, g, row_mode):
+    fp32, _, _ = ops
+    rng = np.random.default_rng(g + row_mode)
+    x = spread(rng, 9, 2560)
+    x[1] = 0
+    x[2, 5] = np.float32(1e-41)
+    x[3, :] = rng.standard_normal(2560).astype(np.float32) * 1e-37   # mostly denormal: flushes
+    x[4, 7] = np.inf
+    say("qact", g, row_mode)
+    q, S, d = fp32.quantize_mx(x, g, row_mode)
+    q0, S0, d0 = F.quantize_mx(x, g, row_mode)
+    assert np.array_equal(q, q0) and same_bits(S, S0) and np.array_equal(d, d0)
+
+
+def test_qact_recip_every_significand(ops):
+    """One row per significand pattern sweep: amax = each value, so S and the quantized
+    values exercise recip over [1, 2) times many exponents."""
+    fp32, _, _ = ops
+    rng = np.random.default_rng(3)
+    amax = F.from_bits(rng.integers(0x00800000, 0x7E000000, 4096).astype(np.uint32))
+    x = (rng.uniform(-1, 1, (4096, 128)) * amax[:, None]).astype(np.float32)
+    x[:, 0] = amax
+    say("qact recip sweep")
+    q, S, d = fp32.quantize_mx(x, 32)
+    q0, S0, d0 = F.quantize_mx(x, 32)
+    assert np.array_equal(q, q0) and same_bits(S, S0) and np.array_equal(d, d0)
+
+
+@pytest.mark.parametrize("fmt,unit,rsc,k0,big", CASES)
+@pytest.mark.parametrize("KB", [1, 3, 8])
+def test_mm_cases(ops, fmt, unit, rsc, k0, big, KB):
+    _, _, mxu = ops
+    for M in (1, 3, 5):
+        c = mm_case(fmt, unit, rsc, k0, big, KB, M=M, N=37)
+        flags = (MM.UNIT if unit else 0) | (MM.RSC if rsc else 0)
+        say("mm", fmt, unit, rsc, k0, big, KB, M)
+        want_acc, _ = MM.mm_acc(c["q"], c["da"], c["rows"], c["srows"], fmt, c["K"], flags=flags, k0=k0)
+        want = MM.mm(c["q"], c["Sa"], c["da"], c["rows"], c["srows"], fmt, c["K"], flags=flags, k0=k0)
+        got = mxu.mm(c["q"], c["Sa"], c["da"], c["rows"], c["srows"], fmt, c["K"], rsc=rsc, unit=unit, k0=k0)
+        acc = mxu.mm_acc(c["q"], c["da"], c["rows"], c["srows"], fmt, c["K"], rsc=rsc, unit=unit, k0=k0)
+        assert np.array_equal(acc, want_acc)
+        assert same_bits(got, want)
+
+
+def test_mm_flags(ops):
+    _, _, mxu = ops
+    rng = np.random.default_rng(6)
+    c = mm_case("int8", True, False, 0, False, 4, M=3, N=300)
+    old = rng.standard_normal((3, 300)).astype(np.float32)
+    alpha = rng.standard_normal(3).astype(np.float32)
+    a = (c["q"], c["Sa"], c["da"], c["rows"], c["srows"], "int8", c["K"])
+    say("mm flags")
+    assert same_bits(mxu.mm(*a, unit=True, acc=old), MM.mm(*a, flags=MM.UNIT | MM.ACC, old=old))
+    assert same_bits(mxu.mm(*a, unit=True, acc=old, alpha=alpha),
+                     MM.mm(*a, flags=MM.UNIT | MM.ACC | MM.ASCALE, old=old, alpha=alpha))
+    y, mx = mxu.mm(*a, unit=True, rmax=True)
+    y0, mx0 = MM.mm(*a, flags=MM.UNIT | MM.RMAX)
+    assert same_bits(y, y0) and same_bits(mx, mx0)
+
+
+def test_mm_refuses_what_the_reference_refuses(ops):
+    from opentpu_amd._lib import OtpuError
+    _, _, mxu = ops
+    c = mm_case("nvfp4", False, False, 0, False, 1)
+    with pytest.raises(OtpuError):            # RSC does not take NVFP4
+        mxu.mm(c["q"], c["Sa"], c["da"], c["rows"], c["srows"], "nvfp4", c["K"], rsc=True)
+    c = mm_case("int8", False, False, 0, False, 1)
+    with pytest.raises(OtpuError):            # ASCALE needs UNIT and ACC
+        mxu.mm(c["q"], c["Sa"], c["da"], c["rows"], c["srows"], "int8", c["K"],
+               acc=np.zeros((3, 5), np.float32), alpha=np.ones(3, np.float32))
+    with pytest.raises(OtpuError):            # scale rows too short for k0
+        mxu.mm(c["q"], c["Sa"], c["da"], c["rows"], c["srows"], "int8", c["K"], k0=9)
+
+
+def test_packers(ops):
+    _, quant, _ = ops
+    rng = np.random.default_rng(2)
+    W = spread(rng, 64, 1152, 3.0, 32) * np.float32(0.02)
+    W[3, 128:256] = 0
+    W[5] = 0
+    say("pack int8")
+    r, s = quant.quantize_mxu(W, "int8")
+    r0, s0 = Q.pack_int8x(W)
+    assert np.array_equal(r, r0) and np.array_equal(s, s0)
+    r, s = quant.quantize_mxu(W, "int8", rsc=True)
+    r0, s0 = Q.pack_rsc(W)
+    assert np.array_equal(r, r0) and np.array_equal(s, s0)
+    g = np.load(GOLD)
+    for name in ("c2", "spread", "grid"):
+        for fmt in ("int4", "fp4"):
+            say("pack", name, fmt)
+            r, s = quant.quantize_mxu(g[f"{name}_W"], fmt)
+            assert np.array_equal(r, g[f"{name}_{fmt}_rows"]), (name, fmt)
+            assert np.array_equal(s, g[f"{name}_{fmt}_srows"]), (name, fmt)
+    for fmt in ("int4", "fp4"):
+        Wb = spread(rng, 256, 640, 2.0, 32)
+        say("pack vs oracle", fmt)
+        r, s = quant.quantize_mxu(Wb, fmt)
+        r0, s0 = Q.pack_x4(Wb, fmt)
+        assert np.array_equal(r, r0) and np.array_equal(s, s0)
+
+
+def _config_weights(seed, N, K, fmt, rsc=False):
+    rng = np.random.default_rng(seed)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    if fmt == "int8":
+        rows, srows = Q.pack_rsc(W) if rsc else Q.pack_int8x(W)
+    else:
+        rows, srows = Q.pack_x4(W, fmt)
+    return W, x, rows, srows
+
+
+@pytest.mark.parametrize("name,N,K,fmt,rsc", [("c1 RSC", 4096, 1024, "int8", True),
+                                              ("c1 int8x", 4096, 1024, "int8", False),
+                                              ("c2 int4x", 6144, 2048, "int4", False)])
+def test_configs_full_size(ops, name, N, K, fmt, rsc):
+    _, _, mxu = ops
+    W, x, rows, srows = _config_weights(1, N, K, fmt, rsc)
+    q, Sa, da = F.quantize_mx(x, 32)
+    say("config", name)
+    got = mxu.mm(q, Sa, da, rows, srows, fmt, K, rsc=rsc)
+    want = OC.mm(q, Sa, da, rows, srows, fmt, K, flags=MM.RSC if rsc else 0)
+    assert same_bits(got, want)
+    # the float64 product of the dequantized operands (no group drops at these scales)
+    xa = (q.astype(np.float64).reshape(1, -1, 32) * np.exp2(-da.astype(np.float64))[..., None]
+          ).reshape(1, -1) * np.float64(Sa[0])
+    ref = xa @ Q.dequantize(rows, srows, fmt, K, rsc=rsc).T
+    assert np.abs(got - ref).max() < 1e-5 * np.abs(ref).max()
+
+
+def test_lm_head_argmax_full_size(ops):
+    import torch
+    _, quant, mxu = ops
+    N, K = 262144, 2560
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+    say("lm head c5: pack")
+    rows_d, srows_d = quant.quantize_mxu(W, "int8", rsc=True)
+    del W
+    rows, srows = rows_d.cpu().numpy(), srows_d.cpu().numpy()
+    x = np.random.default_rng(5).standard_normal((1, K)).astype(np.float32)
+    q, Sa, da = F.quantize_mx(x, 32)
+    say("lm head c5")
+    tok, logits, best = mxu.lm_head_argmax(q, Sa, da, rows, srows, "int8", K, rsc=True)
+    want = OC.mm(q, Sa, da, rows, srows, "int8", K, flags=MM.RSC)[0]
+    assert same_bits(logits, want)
+    t0, b0 = OC.argmax(want)
+    assert tok == t0 == MM.greedy(want) and best == b0
+
+
+def test_lm_head_ties_go_to_the_lowest_index(ops):
+    _, _, mxu = ops
+    rng = np.random.default_rng(7)
+    N, K = 5000, 256
+    rows = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    rows[4321] = 127
+    rows[77] = 127                                   # the same logit, earlier
+    rows[4999] = 127
+    srows = np.full((N, 1), 0.01, np.float32).view(np.uint8)
+    x = np.abs(rng.standard_normal((1, K))).astype(np.float32)
+    q, Sa, da = F.quantize_mx(x, 32)
+    say("lm head ties")
+    tok, logits, best = mxu.lm_head_argmax(q, Sa, da, rows.view(np.uint8), srows, "int8", K, rsc=True, base=1000)
+    assert tok == 1077 and MM.greedy(logits) == 77
+
+
+def test_argmax_vop(ops):
+    _, _, mxu = ops
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((5, 300)).astype(np.float32)
+    a[1, [7, 40, 299]] = 9.0
+    a[2] = -np.inf
+    a[2, 250] = -1e30
+    a[3, :] = 0.0
+    a[3, 100] = -0.0
+    a[4, :] = -1.0
+    a[4, 5], a[4, 9] = 1e-41, 0.0
+    say("argmax vop")
+    v, idx = mxu.argmax(a)
+    v0, i0 = MM.argmax(a)
+    assert list(idx) == list(i0) == [int(np.argmax(a[0])), 7, 250, 0, 5]
+    assert same_bits(v, v0)
+
+
+def test_dot_ranges_accumulate_in_order(ops):
+    """Two QACT ranges -> two MMs, the second ACC (compiler.py:2686-2720), as the oracle."""
+    _, _, mxu = ops
+    rng = np.random.default_rng(5)
+    M, N, K = 2, 160, 512
+    x = spread(rng, M, K, 2.0)
+    x[:, 256:] *= 300.0
+    for fmt in ("int8", "int4"):
+        W = (spread(rng, N, K, 2.0) * 0.02).astype(np.float32)
+        rows, srows = Q.pack_int8x(W) if fmt == "int8" else Q.pack_x4(W, fmt)
+        w = mxu.QWeight.from_packed(rows, srows, fmt, K)
+        say("dot ranges", fmt)
+        got = mxu.dot(x, w, ranges=[256, 256])
+        want = None
+        for c0 in (0, 256):
+            q, Sa, da = F.quantize_mx(x[:, c0:c0 + 256], 32)
+            part = MM.mm(q, Sa, da, rows[:, (c0 if fmt == "int8" else c0 // 2):], srows, fmt, 256,
+                         flags=0 if want is None else MM.ACC, k0=c0 // 128, old=want)
+            want = part
+        assert same_bits(np.asarray(got), want)
+
+
+def test_batched_is_independent_mms(ops):
+    import torch
+    _, _, mxu = ops
+    from opentpu_amd import _lib as X
+    rng = np.random.default_rng(8)
+    B, N, K = 5, 96, 1024
+    qs, Sas, das, rs, ss, want = [], [], [], [], [], []
+    for b in range(B):
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        x = rng.standard_normal((1, K)).astype(np.float32)
+        r, s = Q.pack_x4(W, "int4")
+        q, Sa, da = F.quantize_mx(x, 32)
+        qs.append(q); Sas.append(Sa); das.append(da); rs.append(r); ss.append(s)
+        want.append(MM.mm(q, Sa, da, r, s, "int4", K))
+    qd = torch.from_numpy(np.concatenate(qs)).cuda()
+    Sad = torch.from_numpy(np.concatenate(Sas)).cuda()
+    dad = torch.from_numpy(np.concatenate(das)).cuda()
+    rd = torch.from_numpy(np.concatenate(rs)).cuda()
+    sd = torch.from_numpy(np.concatenate(ss)).cuda()
+    out = torch.empty((B, 1, N), dtype=torch.float32, device="cuda")
+    say("batched")
+    X.call("otpu_mm_batched", B, X.ptr(qd), K, K, X.ptr(Sad), 1, X.ptr(dad), K // 32, K // 32, 1, K,
+           X.ptr(rd), rd.shape[1], N * rd.shape[1], X.ptr(sd), sd.shape[1], N * sd.shape[1], N, X.FMT["int4"],
+           0, 0, X.ptr(out), N, N, X.stream())
+    got = out.cpu().numpy()
+    for b in range(B):
+        assert same_bits(got[b], want[b])
