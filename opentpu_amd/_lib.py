@@ -11,7 +11,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libotpu_amd.so")
+LIB_PATH = os.environ.get("OTPU_LIB") or os.path.join(HERE, "libotpu_amd.so")
 
 INT8, INT4, FP4, NVFP4 = 0, 1, 2, 3
 FMT = {"int8": INT8, "int4": INT4, "fp4": FP4, "nvfp4": NVFP4}

@@ -14,6 +14,8 @@
 // then B = m << (W - dw - da) (0 where the shift is negative) and an int64 multiply-add.  The
 // wave reduces each row's int64 partials with shuffles and R*M lanes run the fp32 epilogue
 // (three FTZ products) and store.  Scale rows are read per lane piece (4 lanes share a word).
+#include <cstdlib>
+
 #include "otpu_common.h"
 
 namespace otpu {
@@ -43,8 +45,12 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // a streamed 16-byte weight load, marked non-temporal (the rows are read once)
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) {
+#if OTPU_GEMV_NT
     u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *reinterpret_cast<const uint4*>(p);
+#endif
 }
 
 // E2M1 codes (4 per dword, one per byte, 0..15) -> signed int8 values, twice the E2M1 value
@@ -124,17 +130,29 @@ __device__ __forceinline__ int64_t piece_term(int c0, int c1, uint32_t sc, int s
 }
 
 // rows a team takes per iteration: about four 16-byte loads in flight per lane
+#ifndef OTPU_GEMV_R1
+#define OTPU_GEMV_R1 8
+#endif
+#ifndef OTPU_GEMV_NT
+#define OTPU_GEMV_NT 1
+#endif
+constexpr int rows_per_team_rt(int L) { return L >= 4 ? 1 : (L == 1 ? OTPU_GEMV_R1 : 2); }
 template <int L>
-constexpr int rows_per_team() { return L >= 4 ? 1 : (L == 1 ? 4 : 2); }
+constexpr int rows_per_team() { return rows_per_team_rt(L); }
 
 // activation registers a lane holds: MR rows x L pieces x (4 int8 | 8 split 4-bit) dwords
+// ... and the reduce-scatter needs the R * MR sums of an iteration to fit a team of 16 lanes
+constexpr bool fits_rt(int fmt, int mr, int L) {
+    return mr * L * (fmt == OTPU_INT8 ? 4 : 8) <= 64 && rows_per_team_rt(L) * mr <= 16;
+}
 template <int FMT, int MR, int L>
-constexpr bool fits() { return MR * L * (FMT == OTPU_INT8 ? 4 : 8) <= 64; }
+constexpr bool fits() { return fits_rt(FMT, MR, L); }
 
 template <int FMT, int MR, int L>
 __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
     constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
     constexpr int R = rows_per_team<L>();
+    constexpr int E = R * MR;                             // sums a lane carries per iteration
     const int lane = threadIdx.x & 63;
     const int T = a.T, NT = 64 / T;                       // lanes per team, teams per wave
     const int tl = lane & (T - 1), team = lane / T;
@@ -186,12 +204,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int RW = R * NT;                      // rows a wave takes per iteration
+    const int stride = nwaves * RW;
     uint64_t best = 0;
-    const int er = tl / MR, ej = tl % MR;       // epilogue lane tl = r * MR + j of its team
+    // After the reduce-scatter below, value e = r * MR + j of a team sits in the lanes
+    // tl = e * (T / E) .. (e + 1) * (T / E) - 1; the first of them runs its epilogue.
+    const int span = T / E;
+    const int ee = tl / span;
+    const int er = ee / MR, ej = ee % MR;
+    const bool epilane = (tl % span) == 0;
 
-    for (int n0 = wave * RW; n0 < a.N; n0 += nwaves * RW) {
+    // one iteration's operands: weight pieces, their scale data, the epilogue row's Sw
+    struct Stage {
         uint4 wv[R][L];
         uint32_t sc[R][L];
+        float sw;
+    };
+    auto load = [&](Stage& st, int n0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int n = n0 + r * NT + team;
@@ -201,16 +229,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
             for (int i = 0; i < L; ++i) {
                 const int p = i * T + tl;
                 const bool ok = p < P && n < a.N;
-                wv[r][i] = ok ? ld16(row + 16 * p) : make_uint4(0, 0, 0, 0);
-                sc[r][i] = ok ? piece_scale<FMT>(srow, a.k0, p, plain) : 0u;
+                st.wv[r][i] = ok ? ld16(row + 16 * p) : make_uint4(0, 0, 0, 0);
+                st.sc[r][i] = ok ? piece_scale<FMT>(srow, a.k0, p, plain) : 0u;
             }
         }
-        const int n = n0 + er * NT + team;     // this lane's epilogue output row
-        const bool epi = tl < R * MR && n < a.N && ej < a.M;
-        float sw = 1.0f;
-        if (epi && !unit) sw = *reinterpret_cast<const float*>(ws + (int64_t)n * a.srs);
-
-        int64_t mine = 0;
+        const int n = n0 + er * NT + team;
+        st.sw = (epilane && n < a.N && !unit) ? *reinterpret_cast<const float*>(ws + (int64_t)n * a.srs) : 1.0f;
+    };
+    auto compute = [&](const Stage& st, int n0) {
+        int64_t v[E];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
 #pragma unroll
@@ -219,23 +246,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
 #pragma unroll
                 for (int i = 0; i < L; ++i) {
                     int c0, c1;
-                    piece_dot<FMT>(wv[r][i], act[j][i], c0, c1);
-                    acc += piece_term<FMT>(c0, c1, sc[r][i], shA[j][i], i * T + tl, plain);
+                    piece_dot<FMT>(st.wv[r][i], act[j][i], c0, c1);
+                    acc += piece_term<FMT>(c0, c1, st.sc[r][i], shA[j][i], i * T + tl, plain);
                 }
-                for (int o = T >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-                if (tl == r * MR + j) mine = acc;
+                v[r * MR + j] = acc;
             }
         }
-        if (epi) {
+        // reduce-scatter over the team: each step halves the values a lane carries (E - 1
+        // shuffles in all), then plain xor steps finish the sums over the team's T lanes
+        int o = T >> 1;
+#pragma unroll
+        for (int h = E / 2; h >= 1; h >>= 1, o >>= 1) {
+            const bool up = (tl & o) != 0;
+#pragma unroll
+            for (int i = 0; i < h; ++i) {
+                const int64_t keep = up ? v[i + h] : v[i];
+                const int64_t give = up ? v[i] : v[i + h];
+                v[i] = keep + __shfl_xor(give, o, 64);
+            }
+        }
+        int64_t tot = v[0];
+        for (; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+        const int n = n0 + er * NT + team;
+        if (epilane && n < a.N && ej < a.M) {
             if (a.acc_out) {
-                a.acc_out[(int64_t)ej * a.N + n] = mine;
+                a.acc_out[(int64_t)ej * a.N + n] = tot;
             } else {
-                float y = fmul(fmul(i2f(mine), sw), sa2[ej]);
+                float y = fmul(fmul(i2f(tot), st.sw), sa2[ej]);
                 if (out) {
-                    float* o = out + (int64_t)ej * a.ors + n;
-                    if (a.flags & OTPU_ASCALE) y = fadd(fmul(*o, a.alpha[ej]), y);
-                    else if (a.flags & OTPU_ACC) y = fadd(*o, y);
-                    *o = y;
+                    float* op = out + (int64_t)ej * a.ors + n;
+                    if (a.flags & OTPU_ASCALE) y = fadd(fmul(*op, a.alpha[ej]), y);
+                    else if (a.flags & OTPU_ACC) y = fadd(*op, y);
+                    *op = y;
                 }
                 if (a.flags & OTPU_RMAX) atomicMax(a.rmax_key + ej, fkey(y));
                 if (a.best) {
@@ -244,10 +286,29 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
                 }
             }
         }
+    };
+
+    // two stages in flight: the next iteration's loads are issued before this one's math
+    Stage s0, s1;
+    int n0 = wave * RW;
+    if (n0 < a.N) load(s0, n0);
+    for (; n0 < a.N; n0 += 2 * stride) {
+        if (n0 + stride < a.N) load(s1, n0 + stride);
+        compute(s0, n0);
+        if (n0 + stride >= a.N) break;
+        if (n0 + 2 * stride < a.N) load(s0, n0 + 2 * stride);
+        compute(s1, n0 + stride);
     }
-    if (a.best) {                               // one atomic per wave
+    if (a.best) {                               // one atomic per workgroup
+        __shared__ uint64_t red[4];
         best = wave_max_u64(best);
-        if (lane == 0 && best) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)best);
+        if (lane == 0) red[threadIdx.x >> 6] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t m = red[0];
+            for (int i = 1; i < (int)(blockDim.x >> 6); ++i) m = red[i] > m ? red[i] : m;
+            if (m) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)m);
+        }
     }
 }
 
@@ -332,13 +393,29 @@ static int check_mm(const char* who, const int8_t* q, int64_t ldq, const uint8_t
     return OTPU_OK;
 }
 
+// resident workgroups per CU the streaming grid aims for: 12 for one piece a lane (short rows,
+// more waves), else 8 (measured on MI355X); OTPU_GEMV_BLOCKS_PER_CU overrides
+static int gemv_blocks_per_cu(int L) {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("OTPU_GEMV_BLOCKS_PER_CU");
+        int x = e ? atoi(e) : 0;
+        v = (x > 0 && x <= 64) ? x : 0;
+    }
+    return v ? v : (L == 1 ? 12 : 8);
+}
+
 template <int FMT, int MR, int L>
 static void launch_one(const MMArgs& a, int batch, hipStream_t s) {
+    static_assert(fits<FMT, 1, L>(), "one activation row always fits");
     if constexpr (fits<FMT, MR, L>()) {
         constexpr int R = rows_per_team<L>();
         const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
+        // about 8 resident workgroups per CU over the whole batch; each wave then streams
+        // many row groups (its activation registers are loaded once)
         int64_t blocks = (waves + 3) / 4;
-        const int64_t cap = (int64_t)otpu_cu_count() * 8;
+        int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L) / batch;
+        if (cap < 1) cap = 1;
         if (blocks > cap) blocks = cap;
         gemv_kernel<FMT, MR, L><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
     }
@@ -377,8 +454,7 @@ static void pick_team(int P, int* T, int* L) {
 }
 
 static int mr_max(int fmt, int L) {
-    const int aw = fmt == OTPU_INT8 ? 4 : 8;
-    return 4 * L * aw <= 64 ? 4 : (2 * L * aw <= 64 ? 2 : 1);
+    return fits_rt(fmt, 4, L) ? 4 : (fits_rt(fmt, 2, L) ? 2 : 1);
 }
 
 static int launch_gemv(MMArgs a, int fmt, int batch, hipStream_t s) {
