@@ -494,8 +494,8 @@ static MMArgs make_args(const int8_t* q, int64_t ldq, const float* Sa, const uin
 }
 
 int otpu_gemm_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda, int M, int K,
-                  const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
-                  float* out, int64_t ors, hipStream_t s);
+                  const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
+                  const float* alpha, float* out, int64_t ors, hipStream_t s);
 
 extern "C" int otpu_mm(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda,
                        int M, int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N,
@@ -507,8 +507,9 @@ extern "C" int otpu_mm(const int8_t* q, int64_t ldq, const float* Sa, const uint
     if ((flags & OTPU_ASCALE) && !alpha) return otpu_fail(OTPU_EINVAL, "mm: ASCALE without alpha");
     if ((flags & OTPU_RMAX) && !rowmax) return otpu_fail(OTPU_EINVAL, "mm: RMAX without rowmax");
     hipStream_t s = (hipStream_t)stream;
-    if (M > 4 && !(flags & (OTPU_ACC | OTPU_ASCALE | OTPU_RMAX)) && k0 == 0) {
-        rc = otpu_gemm_try(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, fmt, flags, out, ors, s);
+    if (M > 4) {
+        rc = otpu_gemm_try(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, fmt, flags & ~OTPU_PAIR, k0, alpha,
+                           out, ors, s);
         if (rc <= 0) return rc;                       // handled (or failed); > 0: not this path
     }
     MMArgs a = make_args(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, flags, k0);

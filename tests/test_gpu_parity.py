@@ -272,3 +272,78 @@ def test_batched_is_independent_mms(ops):
     got = out.cpu().numpy()
     for b in range(B):
         assert same_bits(got[b], want[b])
+
+
+GEMM_CASES = [  # M, N, K, weights (rsc | int8x | unit), activations (row | mx | wide), k0
+    (512, 384, 2048, "rsc", "row", 0),
+    (200, 300, 1024, "rsc", "mx", 0),
+    (130, 257, 512, "int8x", "mx", 0),
+    (64, 128, 384, "int8x", "row", 2),
+    (96, 160, 256, "unit", "mx", 0),
+    (128, 128, 2048, "rsc", "wide", 0),      # offsets over > 6 binades: the VALU tiles
+    (40, 70, 640, "int8x", "wide", 1),       # drops (d + e > 16) inside the planes
+]
+
+
+@pytest.mark.parametrize("M,N,K,wk,ak,k0", GEMM_CASES)
+def test_gemm(ops, M, N, K, wk, ak, k0):
+    _, _, mxu = ops
+    rng = np.random.default_rng(M + N + K)
+    if ak == "row":
+        x = rng.standard_normal((M, K)).astype(np.float32)
+    elif ak == "mx":
+        x = spread(rng, M, K, 1.0, 32)
+    else:
+        x = spread(rng, M, K, 7.0, 32)
+    q, Sa, da = F.quantize_mx(x, 32, row_mode=(ak == "row"))
+    KBr = K // 128 + k0
+    W = (spread(rng, N, KBr * 128, 1.5, 128) * 0.02).astype(np.float32)
+    if wk == "rsc":
+        rows, srows = Q.pack_rsc(W)
+    else:
+        rows, srows = Q.pack_int8x(W)
+        if ak == "wide":
+            srows[:, 4:4 + KBr] = rng.integers(0, 20, (N, KBr))     # large dw: more drops
+    rows = np.ascontiguousarray(rows[:, k0 * 128:k0 * 128 + K])
+    flags = MM.RSC if wk == "rsc" else (MM.UNIT if wk == "unit" else 0)
+    say("gemm", M, N, K, wk, ak, k0)
+    got = mxu.mm(q, Sa, da, rows, srows, "int8", K, rsc=wk == "rsc", unit=wk == "unit", k0=k0)
+    want = OC.mm(q, Sa, da, rows, srows, "int8", K, flags=flags, k0=k0)
+    assert same_bits(got, want)
+
+
+def test_gemm_acc_ascale(ops):
+    _, _, mxu = ops
+    rng = np.random.default_rng(9)
+    M, N, K = 72, 200, 512
+    x = spread(rng, M, K, 1.0, 32)
+    q, Sa, da = F.quantize_mx(x, 32)
+    wel = rng.integers(-127, 128, (N, K)).astype(np.int8).view(np.uint8)
+    srows = np.zeros((N, 8), np.uint8)
+    old = rng.standard_normal((M, N)).astype(np.float32)
+    alpha = rng.standard_normal(M).astype(np.float32)
+    say("gemm acc / ascale")
+    got = mxu.mm(q, Sa, da, wel, srows, "int8", K, unit=True, acc=old)
+    assert same_bits(got, OC.mm(q, Sa, da, wel, srows, "int8", K, flags=MM.UNIT | MM.ACC, old=old))
+    got = mxu.mm(q, Sa, da, wel, srows, "int8", K, unit=True, acc=old, alpha=alpha)
+    assert same_bits(got, OC.mm(q, Sa, da, wel, srows, "int8", K, flags=MM.UNIT | MM.ACC | MM.ASCALE,
+                                old=old, alpha=alpha))
+
+
+def test_gemm_c3_full_size(ops):
+    """c3: M=512 x K=2048 x N=8192, ROW activations x RSC weights (the headline GEMM) and MX
+    activations (the plane path), every output bit against the C oracle."""
+    import torch
+    _, quant, mxu = ops
+    M, K, N = 512, 2048, 8192
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    Wd = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+    rows_d, srows_d = quant.quantize_mxu(Wd, "int8", rsc=True)
+    rows, srows = rows_d.cpu().numpy(), srows_d.cpu().numpy()
+    x = np.random.default_rng(3).standard_normal((M, K)).astype(np.float32)
+    for row_mode in (True, False):
+        q, Sa, da = F.quantize_mx(x, 32, row_mode=row_mode)
+        say("gemm c3", "row" if row_mode else "mx")
+        got = mxu.mm(q, Sa, da, rows, srows, "int8", K, rsc=True)
+        want = OC.mm(q, Sa, da, rows, srows, "int8", K, flags=MM.RSC)
+        assert same_bits(got, want)
