@@ -43,13 +43,30 @@ def c5_bytes(N=262144, K=2560):
     return N * K + 4 * N + K + K // 32 + 4 + 4 * N
 
 
-def timed(fn, steps, warmup, stream):
+def timed(fn, steps, warmup, stream, graph=True):
+    """ms per call of fn (which queues HIP kernels on the current stream).  With graph=True the
+    `steps` calls are captured once in a HIP graph and the replay is timed with HIP events on
+    the stream the kernels run on, so host launch overhead does not pad short kernels."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(steps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        s = torch.cuda.current_stream()
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) / steps
     e0.record(stream)
     for _ in range(steps):
         fn()
@@ -87,28 +104,30 @@ def batched_gemv(fmt, B, N, K, seed, steps, warmup, rsc=False):
     out = torch.empty((B, N), dtype=torch.float32, device="cuda")
     rs, srs = rows.shape[2], srows.shape[2]
     fl = X.RSC if rsc else 0
-    st = X.stream()
 
     def step():
         X.call("otpu_mm_batched", B, X.ptr(q), K, K, X.ptr(Sa), 1, X.ptr(da), K // 32, K // 32, 1, K,
-               X.ptr(rows), rs, N * rs, X.ptr(srows), srs, N * srs, N, X.FMT[fmt], fl, 0, X.ptr(out), N, N, st)
+               X.ptr(rows), rs, N * rs, X.ptr(srows), srs, N * srs, N, X.FMT[fmt], fl, 0, X.ptr(out), N, N, X.stream())
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
-    single = rows[0], srows[0], q[:1], Sa[:1], da[:1]
-    return ms, single
+    return ms, (rows, srows, q, Sa, da)
 
 
-def single_gemv_ms(fmt, single, N, K, steps, rsc=False):
-    """One GEMV per launch, cycling over weight copies held by the batch (not cache-resident)."""
+def single_gemv_ms(fmt, batch, N, K, steps, rsc=False):
+    """One GEMV per launch, each launch on the next of the batch's weight sets (more than the
+    Infinity Cache holds in all, so every launch streams its weights from HBM)."""
     import torch
 
     from opentpu_amd import _lib as X
-    rows, srows, q, Sa, da = single
+    rows, srows, q, Sa, da = batch
+    B = rows.shape[0]
     out = torch.empty((1, N), dtype=torch.float32, device="cuda")
-    st = X.stream()
+    it = [0]
 
     def step():
-        X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, 1, K, X.ptr(rows), rows.shape[1],
-               X.ptr(srows), srows.shape[1], N, X.FMT[fmt], X.RSC if rsc else 0, 0, None, X.ptr(out), N, None, st)
+        b = it[0] % B
+        it[0] += 1
+        X.call("otpu_mm", X.ptr(q[b]), K, X.ptr(Sa[b]), X.ptr(da[b]), K // 32, 1, K, X.ptr(rows[b]), rows.shape[2],
+               X.ptr(srows[b]), srows.shape[2], N, X.FMT[fmt], X.RSC if rsc else 0, 0, None, X.ptr(out), N, None, X.stream())
     return timed(step, steps, 3, torch.cuda.current_stream())
 
 
@@ -127,11 +146,10 @@ def lm_head(steps, warmup):
     logits = torch.empty((N,), dtype=torch.float32, device="cuda")
     best = torch.empty((1,), dtype=torch.int64, device="cuda")
     tok = torch.empty((1,), dtype=torch.int32, device="cuda")
-    st = X.stream()
 
     def step():
         X.call("otpu_lm_head_argmax", X.ptr(q), X.ptr(Sa), X.ptr(da), K, X.ptr(rows), K, X.ptr(srows), 4, N,
-               X.FMT["int8"], X.RSC, 0, 0, X.ptr(logits), X.ptr(best), X.ptr(tok), st)
+               X.FMT["int8"], X.RSC, 0, 0, X.ptr(logits), X.ptr(best), X.ptr(tok), X.stream())
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
     return ms, int(tok.item())
 
@@ -148,11 +166,10 @@ def gemm(steps, warmup):
     x = torch.randn((M, K), generator=gen, device="cuda")
     q, Sa, da = fp32.quantize_mx(x, 32, row_mode=True)
     out = torch.empty((M, N), dtype=torch.float32, device="cuda")
-    st = X.stream()
 
     def step():
         X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, M, K, X.ptr(rows), K, X.ptr(srows), 4, N,
-               X.FMT["int8"], X.RSC, 0, None, X.ptr(out), N, None, st)
+               X.FMT["int8"], X.RSC, 0, None, X.ptr(out), N, None, X.stream())
     return timed(step, steps, warmup, torch.cuda.current_stream())
 
 

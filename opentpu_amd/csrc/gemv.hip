@@ -96,14 +96,14 @@ __device__ __forceinline__ void piece_dot(const uint4 wv, const uint32_t* a, int
     }
 }
 
-// the scale data a piece of row `srow` needs (UNIT / RSC: none)
+// the scale data a piece needs, from the scale row at byte offset ro of base sb (UNIT / RSC: none)
 template <int FMT>
-__device__ __forceinline__ uint32_t piece_scale(const uint8_t* srow, int k0, int p, bool plain) {
+__device__ __forceinline__ uint32_t piece_scale(const uint8_t* sb, uint32_t ro, int k0, int p, bool plain) {
     if (plain) return 0;
-    if (FMT == OTPU_INT8) return srow[4 + k0 + (p >> 3)];
+    if (FMT == OTPU_INT8) return sb[ro + (uint32_t)(4 + k0 + (p >> 3))];
     if (FMT == OTPU_NVFP4)
-        return *reinterpret_cast<const uint16_t*>(srow + 16 + 8 * (k0 + (p >> 2)) + 2 * (p & 3));
-    return *reinterpret_cast<const uint32_t*>(srow + 8 + 4 * (k0 + (p >> 2)));
+        return *reinterpret_cast<const uint16_t*>(sb + (ro + (uint32_t)(16 + 8 * (k0 + (p >> 2)) + 2 * (p & 3))));
+    return *reinterpret_cast<const uint32_t*>(sb + (ro + (uint32_t)(8 + 4 * (k0 + (p >> 2)))));
 }
 
 // B * c for the piece's group(s); shA = W - da of the piece's 32-group (activation side)
@@ -201,7 +201,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
 #pragma unroll
     for (int j = 0; j < MR; ++j) sa2[j] = (j < a.M && !a.acc_out) ? fmul(Sa[j], pow2f(-W)) : 0.0f;
 
-    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    // wave-uniform by construction; readfirstlane tells the compiler (scalar loop, no exec masks)
+    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const int RW = R * NT;                      // rows a wave takes per iteration
     const int stride = nwaves * RW;
@@ -219,22 +220,28 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
         uint32_t sc[R][L];
         float sw;
     };
+    // operand addresses: a wave-uniform row-group base (scalar registers) plus 32-bit lane
+    // offsets, so the loads take the saddr + voffset form; rows past N read the last row and
+    // pieces past P the last piece (no branch around a load): the former reach no epilogue, the
+    // latter meet zero activation registers
     auto load = [&](Stage& st, int n0) {
+        const uint8_t* wb = w + (int64_t)n0 * a.rs;
+        const uint8_t* sb = ws + (int64_t)n0 * a.srs;
+        const int last = a.N - 1 - n0;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int n = n0 + r * NT + team;
-            const uint8_t* row = w + (int64_t)n * a.rs;
-            const uint8_t* srow = ws + (int64_t)n * a.srs;
+            const int dn = min(r * NT + team, last);
+            const uint32_t roff = (uint32_t)dn * (uint32_t)a.rs;
+            const uint32_t soff = (uint32_t)dn * (uint32_t)a.srs;
 #pragma unroll
             for (int i = 0; i < L; ++i) {
                 const int p = i * T + tl;
-                const bool ok = p < P && n < a.N;
-                st.wv[r][i] = ok ? ld16(row + 16 * p) : make_uint4(0, 0, 0, 0);
-                st.sc[r][i] = ok ? piece_scale<FMT>(srow, a.k0, p, plain) : 0u;
+                const int pc = p < P ? p : P - 1;
+                st.wv[r][i] = ld16(wb + (roff + 16u * (uint32_t)pc));
+                st.sc[r][i] = piece_scale<FMT>(sb, soff, a.k0, pc, plain);
             }
         }
-        const int n = n0 + er * NT + team;
-        st.sw = (epilane && n < a.N && !unit) ? *reinterpret_cast<const float*>(ws + (int64_t)n * a.srs) : 1.0f;
+        st.sw = unit ? 1.0f : *reinterpret_cast<const float*>(sb + (uint32_t)min(er * NT + team, last) * (uint32_t)a.srs);
     };
     auto compute = [&](const Stage& st, int n0) {
         int64_t v[E];
@@ -288,16 +295,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
         }
     };
 
-    // two stages in flight: the next iteration's loads are issued before this one's math
-    Stage s0, s1;
-    int n0 = wave * RW;
-    if (n0 < a.N) load(s0, n0);
-    for (; n0 < a.N; n0 += 2 * stride) {
-        if (n0 + stride < a.N) load(s1, n0 + stride);
-        compute(s0, n0);
-        if (n0 + stride >= a.N) break;
-        if (n0 + 2 * stride < a.N) load(s0, n0 + 2 * stride);
-        compute(s1, n0 + stride);
+    // one stage per wave: the loads of an iteration go out together and the waves of the SIMD
+    // (5-8 resident) overlap each other's memory latency; a second register stage per wave
+    // costs occupancy and measured slower on MI355X
+    for (int n0 = wave * RW; n0 < a.N; n0 += stride) {
+        Stage st;
+        load(st, n0);
+        compute(st, n0);
     }
     if (a.best) {                               // one atomic per workgroup
         __shared__ uint64_t red[4];
@@ -387,13 +391,15 @@ static int check_mm(const char* who, const int8_t* q, int64_t ldq, const uint8_t
     }
     if (!al(w, 16) || rs % 16 || !al(q, 16) || ldq % 16)
         return otpu_fail(OTPU_EALIGN, "%s: weight rows and activations 16-byte aligned (w, rs, q, ldq)", who);
+    if (rs >= (1 << 24) || srs >= (1 << 24))
+        return otpu_fail(OTPU_EINVAL, "%s: row strides of 16 MiB or more", who);
     if ((rowb / 16 + 63) / 64 > LMAX)
         return otpu_fail(OTPU_EINVAL, "%s: K %d exceeds the register-resident operand (%d 16-byte pieces a lane)",
                          who, K, LMAX);
     return OTPU_OK;
 }
 
-// resident workgroups per CU the streaming grid aims for: 12 for one piece a lane (short rows,
+// resident workgroups per CU the streaming grid aims for: 16 for one piece a lane (short rows,
 // more waves), else 8 (measured on MI355X); OTPU_GEMV_BLOCKS_PER_CU overrides
 static int gemv_blocks_per_cu(int L) {
     static int v = -1;
@@ -402,7 +408,7 @@ static int gemv_blocks_per_cu(int L) {
         int x = e ? atoi(e) : 0;
         v = (x > 0 && x <= 64) ? x : 0;
     }
-    return v ? v : (L == 1 ? 12 : 8);
+    return v ? v : (L == 1 ? 16 : 8);
 }
 
 template <int FMT, int MR, int L>
