@@ -173,6 +173,92 @@ def gemm(steps, warmup):
     return timed(step, steps, warmup, torch.cuda.current_stream())
 
 
+def c4_step(steps, warmup):
+    """The chained decode step (28 Qwen3-0.6B-shaped layers of int4x linears, weights seeded
+    100 + layer): two resident copies of the weights (474 MB, more than the Infinity Cache),
+    steps alternating between them, every step's kernels replayed from one HIP graph."""
+    import torch
+
+    from opentpu_amd.chain import DecodeChain, Shape
+    sh = Shape()
+    chains = [DecodeChain.synthetic(sh, "int4", seed0=100) for _ in range(2)]
+    x = torch.randn((1, sh.hidden), generator=torch.Generator(device="cuda").manual_seed(4), device="cuda")
+    for c in chains:
+        c.x.copy_(x)
+    it = [0]
+
+    def step():
+        chains[it[0] % 2].step()
+        it[0] += 1
+    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    wb = sh.layers * sh.layer_bytes("int4")
+    launches = sh.layers * DecodeChain.KERNELS_PER_LAYER
+    del chains
+    torch.cuda.empty_cache()
+    return {"us_per_step": round(ms * 1e3, 2), "weight_bytes": wb, "GBps": round(wb / (ms * 1e-3) / 1e9, 1),
+            "kernels_per_step": launches}
+
+
+def copy_calibration(nbytes=1 << 30, reps=3):
+    """A plain streaming copy of nbytes (torch's elementwise neg: one dispatch that reads and
+    writes nbytes), the yardstick the FETCH_SIZE / WRITE_SIZE counters are scaled by: what they
+    read for a copy of known size.  Returns GB/s of read + write."""
+    import torch
+    a = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    ms = timed(lambda: torch.neg(a, out=b), reps, 1, torch.cuda.current_stream(), graph=False)
+    del a, b
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "ms": round(ms, 4), "GBps_rw": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_c2_gemv_int4_batched.txt")
+
+
+def measured_traffic():
+    """HBM bytes per dispatch of the headline kernel as the committed counter summary states it
+    (FETCH_SIZE and WRITE_SIZE scaled by the copy kernel's readings), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_dispatch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def summarize(outdir):
+    """Text summary of rocprofv3 CSV output in outdir (kernel stats, and for counter runs each
+    kernel's mean counter value per dispatch), for the profiles/ folder."""
+    import csv
+    import glob
+    import collections
+    for path in sorted(glob.glob(os.path.join(outdir, "**", "*kernel_stats.csv"), recursive=True)):
+        print(f"# {os.path.relpath(path, outdir)}")
+        with open(path) as f:
+            rows = list(csv.DictReader(f))
+        print(f"{'calls':>7} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>6}  kernel")
+        for r in rows:
+            name = r["Name"].split("(")[0]
+            print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:10.3f} {float(r['MinNs']) / 1e3:10.3f} "
+                  f"{float(r['MaxNs']) / 1e3:10.3f} {float(r['Percentage']):6.2f}  {name[:110]}")
+    for path in sorted(glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True)):
+        print(f"# {os.path.relpath(path, outdir)}")
+        agg = collections.defaultdict(lambda: collections.defaultdict(float))
+        disp = collections.defaultdict(set)
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                key = (r["Kernel_Name"].split("(")[0][:90], r.get("Grid_Size", ""))
+                agg[key][r["Counter_Name"]] += float(r["Counter_Value"])
+                disp[key].add(r["Dispatch_Id"])
+        print(f"{'dispatches':>10}  {'grid':>10}  counter means per dispatch  kernel")
+        for key, d in agg.items():
+            n = len(disp[key])
+            means = ", ".join(f"{c} {v / n:.1f}" for c, v in sorted(d.items()))
+            print(f"{n:10d}  {key[1]:>10}  {means}  {key[0]}")
+
+
 def cpu_baseline(seconds=10.0):
     """The C oracle (OpenMP) on this host: one c2 GEMV repeated for about `seconds`."""
     from oracle import cpu as OC
@@ -205,8 +291,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=80)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of c1,c2,c3,c5 (default: all)")
+    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c4,c5,copy (default: c1,c2s,c3,c4,c5); "
+                    "the headline c2 always runs, c2s adds its single-launch figure")
+    ap.add_argument("--summarize", metavar="DIR", help="print a text summary of rocprofv3 CSV output and exit")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
         sys.exit(2)
@@ -215,18 +306,23 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
-    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3", "c5"}
+    only = set(args.only.split(",")) if args.only else {"c1", "c2s", "c3", "c4", "c5"}
     extra = {}
 
     N2, K2, B2 = 6144, 2048, args.batch
     ms2, single2 = batched_gemv("int4", B2, N2, K2, 2, args.steps, args.warmup)
     gbs2 = B2 * c2_bytes() / (ms2 * 1e-3) / 1e9
     print(f"[c2] batched int4 GEMV: {ms2:.4f} ms/step, {gbs2:.1f} GB/s", file=sys.stderr, flush=True)
-    ms2s = single_gemv_ms("int4", single2, N2, K2, 200)
-    extra["c2_single_launch"] = {"us": round(ms2s * 1e3, 3), "GBps": round(c2_bytes() / (ms2s * 1e-3) / 1e9, 1)}
+    if "c2s" in only:
+        ms2s = single_gemv_ms("int4", single2, N2, K2, 200)
+        extra["c2_single_launch"] = {"us": round(ms2s * 1e3, 3),
+                                     "GBps": round(c2_bytes() / (ms2s * 1e-3) / 1e9, 1)}
     del single2
     torch.cuda.empty_cache()
 
+    if "copy" in only:
+        extra["copy_1GiB"] = copy_calibration()
+        print(f"[copy] {extra['copy_1GiB']}", file=sys.stderr, flush=True)
     if "c1" in only:
         B1 = 128
         ms1, s1 = batched_gemv("int8", B1, 4096, 1024, 1, 20, 3, rsc=True)
@@ -244,6 +340,9 @@ def main():
                                       "frac_hbm": round(c5_bytes() / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         torch.cuda.empty_cache()
         print(f"[c5] {extra['c5_lm_head_argmax']}", file=sys.stderr, flush=True)
+    if "c4" in only:
+        extra["c4_decode_step"] = c4_step(10, 2)
+        print(f"[c4] {extra['c4_decode_step']}", file=sys.stderr, flush=True)
     if "c3" in only:
         ms3 = gemm(5, 1)
         tops = 2 * 512 * 2048 * 8192 / (ms3 * 1e-3) / 1e12
@@ -268,7 +367,7 @@ def main():
         "config": {"workload": f"c2: 4-bit int4x group-32 decode GEMV N={N2} K={K2}, {B2} independent "
                                f"weight sets per launch", "batch": B2, "N": N2, "K": K2, "fmt": "int4"},
         "roofline": {"bound": "hbm", "achieved": round(gbs2, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs2 / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs2 / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -58,6 +58,19 @@ int otpu_version(void);
 int otpu_qact(const float* x, int M, int K, int64_t ldx, int g, int row_mode, int8_t* q,
               int64_t ldq, float* S, uint8_t* d, int64_t ldd, otpu_stream_t stream);
 
+/* QACT over K / width equal column ranges of each row in one launch: one QACT instruction per
+ * range (opentpu/isasim.py:927-959), as the reference quantizes a down projection's input in
+ * F-chunks (opentpu/kernels/mlp.py:8-30, :87-120).  Range r of row j: q[j, r*width ..], its
+ * scale S[r * M + j], its offsets d[j, r*width/g ..].  xmul (may be NULL): quantize the VOP MUL
+ * x * xmul instead of x (same shape and stride; the SwiGLU product g * u of mlp.py:101-104). */
+int otpu_qact_ranges(const float* x, const float* xmul, int M, int K, int64_t ldx, int width, int g,
+                     int row_mode, int8_t* q, int64_t ldq, float* S, uint8_t* d, int64_t ldd,
+                     otpu_stream_t stream);
+
+/* VOP MUL (opentpu/isasim.py:1181, V_MUL; fp32.mul, opentpu/fp32.py:100): out = a * b, one IEEE RNE
+ * product with flush-to-zero on operands and result, over n elements. */
+int otpu_vmul(const float* a, const float* b, float* out, int64_t n, otpu_stream_t stream);
+
 /* MM (opentpu/isasim.py:749-910, opentpu/isa.py:502; semantics docs/isa.md:226-305), natural
  * row layout, rows of one:
  *   q [M, ldq] int8, Sa [M], da [M, ldda] uint8 (an offset per 32 of K): the operand one QACT
@@ -78,6 +91,18 @@ int otpu_mm(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, in
 int otpu_mm_acc(const int8_t* q, int64_t ldq, const uint8_t* da, int64_t ldda, int M, int K,
                 const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt,
                 int flags, int k0, int64_t* acc, otpu_stream_t stream);
+
+/* Builder.dot's per-range MMs (opentpu/compiler.py:2686-2720; swiglu_down's chunks,
+ * opentpu/kernels/mlp.py:87-120): K / width MMs, range r over columns r*width .. of q / da
+ * (offsets) and of the weight rows (scale blocks k0 + r*width/128), its activation scale
+ * Sa[r * M + j] (otpu_qact_ranges' layout), accumulated in range order as the ACC chain
+ * out = add(..add(add(old | y_0, y_1)..), y_R-1) (old with ACC; else y_0 starts it).
+ * part: a caller's workspace of R * M * N fp32 (the per-range MM outputs).  width a multiple
+ * of 128 (int8) or 256 (4-bit: ranges start on whole 128-byte chunks).  No ASCALE / RMAX. */
+int otpu_mm_ranges(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda,
+                   int M, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
+                   int64_t srs, int N, int fmt, int flags, int k0, float* part, float* out,
+                   int64_t ors, otpu_stream_t stream);
 
 /* B independent MMs of one shape in one launch (a layer stack's or an expert set's decode
  * GEMVs): problem b's operands start at the given pointers plus b times the *_bstride

@@ -31,6 +31,9 @@ SIGNATURES = {
     "otpu_argmax": ([_P, _I, _I, _L, _L, _P, _L, _P], _I),
     "otpu_pack_int8": ([_P, _I, _I, _L, _I, _P, _L, _P, _L, _P], _I),
     "otpu_pack_x4": ([_P, _I, _I, _L, _I, _P, _L, _P, _L, _P], _I),
+    "otpu_qact_ranges": ([_P, _P, _I, _I, _L, _I, _I, _I, _P, _L, _P, _P, _L, _P], _I),
+    "otpu_mm_ranges": ([_P, _L, _P, _P, _L, _I, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P], _I),
+    "otpu_vmul": ([_P, _P, _P, _L, _P], _I),
 }
 
 

@@ -1,0 +1,180 @@
+"""The chained decode step of a Qwen3-shaped stack of quantized linears, resident on the GPU.
+
+Per layer (the reference's lowering of a decoder layer's linears: `opentpu/kernels/mlp.py`,
+`Builder.dot` `opentpu/compiler.py:2686-2720`):
+    QACT(x) -> MM qkv          q, k, v rows stacked: one weight, one launch
+    QACT(q) -> MM o
+    QACT(o) -> MM gu           gate, up rows stacked
+    QACT ranges of mul(g, u)   the down input in F-chunks (one QACT each, `mlp.py:8-30`)
+            -> MM down         one MM per chunk, ACC in chunk order (otpu_mm_ranges)
+and the down output is the next layer's input.  Every buffer is allocated once; a step only
+queues kernels, so it can be captured in a HIP graph and replayed (`capture` / `replay`).
+
+Weights: one int4x / fp4x6 / int8x packing per linear, packed on the GPU (`quant.quantize_mxu`),
+or the reference's packed bytes loaded unchanged (`from_packed`)."""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib as X
+from .quant import D, quantize_mxu, row_bytes, scale_bytes
+
+
+def down_chunk(f_loc: int, fmt: str) -> int:
+    """The F-chunk each down MM's activations are quantized over (`opentpu/kernels/mlp.py:8-30`):
+    about 8 chunks, a multiple of D (int8) or 2D (4-bit), at least 2D where F allows."""
+    q = D if fmt == "int8" else 2 * D
+    if f_loc % q:
+        raise ValueError(f"F {f_loc} is not a multiple of {q}")
+    lo = min(f_loc, -(-2 * D // q) * q)
+    c = max(lo, (f_loc // 8) // q * q)
+    while f_loc % c and c > lo:
+        c -= q
+    while f_loc % c:
+        c += q
+    return c
+
+
+@dataclass
+class Shape:
+    """A Qwen3-shaped layer's linears (defaults: Qwen3-0.6B: hidden 1024, 16 q heads and 8 kv
+    heads of 128, intermediate 3072, 28 layers)."""
+    hidden: int = 1024
+    q_dim: int = 2048
+    kv_dim: int = 1024
+    F: int = 3072
+    layers: int = 28
+
+    def weight_shapes(self):
+        """(name, N, K) of the four streamed weights of a layer."""
+        h = self.hidden
+        return [("qkv", self.q_dim + 2 * self.kv_dim, h), ("o", h, self.q_dim), ("gu", 2 * self.F, h),
+                ("down", h, self.F)]
+
+    def layer_bytes(self, fmt: str) -> int:
+        return sum(N * (row_bytes(K, fmt) + scale_bytes(K, fmt)) for _, N, K in self.weight_shapes())
+
+
+class DecodeChain:
+    """`layers`: per layer a dict name -> (rows, srows) device tensors (uint8)."""
+
+    KERNELS_PER_LAYER = 9          # 3 QACT, 3 MM, QACT ranges, per-range MM + its ACC chain
+
+    def __init__(self, layers: list, shape: Shape = Shape(), fmt: str = "int4"):
+        self.layers = layers
+        self.shape = shape
+        self.fmt = fmt
+        s = shape
+        self.width = down_chunk(s.F, fmt)
+        self.R = s.F // self.width
+        nq = s.q_dim + 2 * s.kv_dim
+        T = X.torch()
+        dev = "cuda"
+        f32, i8, u8 = T.float32, T.int8, T.uint8
+        self.x = T.zeros((1, s.hidden), dtype=f32, device=dev)
+        self.y = T.zeros((1, s.hidden), dtype=f32, device=dev)           # the step's output
+        self.y2 = T.zeros((1, s.hidden), dtype=f32, device=dev)
+        self.qkv = T.empty((1, nq), dtype=f32, device=dev)
+        self.o = T.empty((1, s.hidden), dtype=f32, device=dev)
+        self.gu = T.empty((1, 2 * s.F), dtype=f32, device=dev)
+        kmax = max(s.hidden, s.q_dim, s.F)
+        self.qa = T.empty((1, kmax), dtype=i8, device=dev)
+        self.Sa = T.empty((self.R,), dtype=f32, device=dev)
+        self.da = T.empty((1, kmax // 32), dtype=u8, device=dev)
+        self.part = T.empty((self.R, s.hidden), dtype=f32, device=dev)
+        self._graph = None
+
+    @staticmethod
+    def synthetic(shape: Shape = Shape(), fmt: str = "int4", seed0: int = 100, std: float = 0.02) -> "DecodeChain":
+        """Random-init weights N(0, std), layer l from a generator seeded seed0 + l (the weights
+        of each linear drawn in the order q, k, v, o, gate, up, down), packed on the GPU."""
+        T = X.torch()
+        layers = []
+        for l in range(shape.layers):
+            g = T.Generator(device="cuda").manual_seed(seed0 + l)
+            h = shape.hidden
+
+            def rnd(n, k):
+                return T.randn((n, k), generator=g, device="cuda") * std
+            Wq, Wk, Wv = rnd(shape.q_dim, h), rnd(shape.kv_dim, h), rnd(shape.kv_dim, h)
+            Wo = rnd(h, shape.q_dim)
+            Wg, Wu = rnd(shape.F, h), rnd(shape.F, h)
+            Wd = rnd(h, shape.F)
+            layers.append({"qkv": quantize_mxu(T.cat([Wq, Wk, Wv]), fmt), "o": quantize_mxu(Wo, fmt),
+                           "gu": quantize_mxu(T.cat([Wg, Wu]), fmt), "down": quantize_mxu(Wd, fmt)})
+            del Wq, Wk, Wv, Wo, Wg, Wu, Wd
+        return DecodeChain(layers, shape, fmt)
+
+    @staticmethod
+    def from_packed(layers: list, shape: Shape = Shape(), fmt: str = "int4") -> "DecodeChain":
+        """Packed (rows, srows) pairs per layer (numpy or tensors), e.g. the reference's
+        quantize_mxu output, loaded unchanged."""
+        out = []
+        for wts in layers:
+            out.append({k: (X.dev(r, np.uint8), X.dev(sr, np.uint8)) for k, (r, sr) in wts.items()})
+        return DecodeChain(out, shape, fmt)
+
+    # --- the kernels of one step ---------------------------------------------------------
+    def _qact(self, x, K: int) -> None:
+        X.call("otpu_qact", X.ptr(x), 1, K, x.stride(0), 32, 0, X.ptr(self.qa), self.qa.shape[1],
+               X.ptr(self.Sa), X.ptr(self.da), self.da.shape[1], X.stream())
+
+    def _mm(self, w, K: int, out) -> None:
+        rows, srows = w
+        X.call("otpu_mm", X.ptr(self.qa), self.qa.shape[1], X.ptr(self.Sa), X.ptr(self.da), self.da.shape[1],
+               1, K, X.ptr(rows), rows.shape[1], X.ptr(srows), srows.shape[1], rows.shape[0],
+               X.FMT[self.fmt], 0, 0, None, X.ptr(out), out.shape[1], None, X.stream())
+
+    def layer(self, l: int, x, y) -> None:
+        """Queue layer l: input x [1, hidden] -> output y [1, hidden]."""
+        s, w = self.shape, self.layers[l]
+        self._qact(x, s.hidden)
+        self._mm(w["qkv"], s.hidden, self.qkv)
+        self._qact(self.qkv, s.q_dim)                     # q: the first q_dim columns
+        self._mm(w["o"], s.q_dim, self.o)
+        self._qact(self.o, s.hidden)
+        self._mm(w["gu"], s.hidden, self.gu)
+        g, u = self.gu[:, :s.F], self.gu[:, s.F:]
+        X.call("otpu_qact_ranges", X.ptr(g), X.ptr(u), 1, s.F, self.gu.shape[1], self.width, 32, 0, X.ptr(self.qa),
+               self.qa.shape[1], X.ptr(self.Sa), X.ptr(self.da), self.da.shape[1], X.stream())
+        rows, srows = w["down"]
+        X.call("otpu_mm_ranges", X.ptr(self.qa), self.qa.shape[1], X.ptr(self.Sa), X.ptr(self.da),
+               self.da.shape[1], 1, s.F, self.width, X.ptr(rows), rows.shape[1], X.ptr(srows), srows.shape[1],
+               rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(self.part), X.ptr(y), y.shape[1], X.stream())
+
+    def _queue(self) -> None:
+        n = len(self.layers)
+        src = self.x
+        for l in range(n):                                # outputs alternate so the last is self.y
+            dst = self.y if (n - 1 - l) % 2 == 0 else self.y2
+            self.layer(l, src, dst)
+            src = dst
+
+    def step(self, x=None):
+        """One decode step on input x [1, hidden] (fp32; default: the last input set):
+        returns the device tensor holding the last layer's output."""
+        if x is not None:
+            self.x.copy_(X.dev(x, np.float32).reshape(1, -1))
+        self._queue()
+        return self.y
+
+    def capture(self) -> None:
+        """Record one step (every layer's kernels) in a HIP graph; `replay` runs it on the
+        current content of self.x."""
+        T = X.torch()
+        self._queue()                                     # warm-up outside the capture
+        T.cuda.synchronize()
+        g = T.cuda.CUDAGraph()
+        with T.cuda.graph(g):
+            self._queue()
+        self._graph = g
+
+    def replay(self, x=None):
+        if self._graph is None:
+            self.capture()
+        if x is not None:
+            self.x.copy_(X.dev(x, np.float32).reshape(1, -1))
+        self._graph.replay()
+        return self.y

@@ -37,8 +37,9 @@ struct MMArgs {
     uint64_t* best;                // LM head: max of (key << 32 | ~index)
     int64_t base;                  // LM head: index of row 0
     int P, T;                      // 16-byte pieces per row, lanes per row (team)
-    // batch strides (elements of each pointer's type; bytes for w / ws)
+    // batch strides (elements of each pointer's type; bytes for w / ws; blocks for k0)
     int64_t q_bs, sa_bs, da_bs, w_bs, ws_bs, out_bs;
+    int k0_bs;
 };
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -163,6 +164,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
     const uint8_t* w = a.w + b * a.w_bs;
     const uint8_t* ws = a.ws + b * a.ws_bs;
     float* out = a.out ? a.out + b * a.out_bs : nullptr;
+    const int k0 = a.k0 + b * a.k0_bs;
     const bool plain = (a.flags & (OTPU_UNIT | OTPU_RSC)) != 0;
     const bool unit = (a.flags & OTPU_UNIT) != 0;
     const int W = window_of(FMT);
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
                 const int p = i * T + tl;
                 const int pc = p < P ? p : P - 1;
                 st.wv[r][i] = ld16(wb + (roff + 16u * (uint32_t)pc));
-                st.sc[r][i] = piece_scale<FMT>(sb, soff, a.k0, pc, plain);
+                st.sc[r][i] = piece_scale<FMT>(sb, soff, k0, pc, plain);
             }
         }
         st.sw = unit ? 1.0f : *reinterpret_cast<const float*>(sb + (uint32_t)min(er * NT + team, last) * (uint32_t)a.srs);
@@ -325,6 +327,19 @@ __global__ void fill_u32(uint32_t* p, int n, uint32_t v) {
 __global__ void rmax_finish(uint32_t* k, int n) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) k[i] = fbits(unkey(k[i]));
+}
+
+// the ACC chain of R partial MM outputs: out = add(..add(add(old | part_0, part_1)..), part_R-1)
+__global__ void sum_parts(const float* __restrict__ part, int64_t pstride, int R, int M, int N, int acc,
+                          float* __restrict__ out, int64_t ors) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)M * N) return;
+    const int j = (int)(i / N), n = (int)(i % N);
+    const float* p = part + (int64_t)j * N + n;
+    float* o = out + (int64_t)j * ors + n;
+    float y = acc ? fadd(*o, p[0]) : p[0];
+    for (int r = 1; r < R; ++r) y = fadd(y, p[r * pstride]);
+    *o = y;
 }
 
 __global__ void best_finish(const uint64_t* best, int32_t* token) {
@@ -564,6 +579,39 @@ extern "C" int otpu_mm_batched(int B, const int8_t* q, int64_t ldq, int64_t q_bs
     a.q_bs = q_bstride; a.sa_bs = sa_bstride; a.da_bs = da_bstride;
     a.w_bs = w_bstride; a.ws_bs = ws_bstride; a.out_bs = out_bstride;
     return launch_gemv(a, fmt, B, (hipStream_t)stream);
+}
+
+extern "C" int otpu_mm_ranges(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda,
+                              int M, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs,
+                              int N, int fmt, int flags, int k0, float* part, float* out, int64_t ors,
+                              otpu_stream_t stream) {
+    const int chunk = fmt == OTPU_INT8 ? OTPU_D : 2 * OTPU_D;
+    if (width < chunk || width % chunk || K % width)
+        return otpu_fail(OTPU_EINVAL, "mm_ranges: ranges of %d over K %d (multiples of %d for this format)", width,
+                         K, chunk);
+    if (flags & (OTPU_ASCALE | OTPU_RMAX)) return otpu_fail(OTPU_EINVAL, "mm_ranges: no ASCALE or RMAX");
+    const int R = K / width;
+    const bool plain = (flags & (OTPU_UNIT | OTPU_RSC)) != 0;
+    int rc = check_mm("mm_ranges", q, ldq, da, ldda, M, width, w, rs, ws, srs, N, fmt, flags & ~OTPU_ACC,
+                      plain ? k0 : k0 + (K - width) / OTPU_D);
+    if (rc) return rc;
+    if (ldq < K || ldda < K / 32 || rs < (fmt == OTPU_INT8 ? K : K / 2))
+        return otpu_fail(OTPU_EINVAL, "mm_ranges: ldq %lld, ldda %lld, rs %lld short of K %d", (long long)ldq,
+                         (long long)ldda, (long long)rs, K);
+    if (!Sa || !part || !out || ors < N) return otpu_fail(OTPU_EINVAL, "mm_ranges: Sa / part / out NULL or ors < N");
+    if (!al(part, 4)) return otpu_fail(OTPU_EALIGN, "mm_ranges: part");
+    hipStream_t s = (hipStream_t)stream;
+    MMArgs a = make_args(q, ldq, Sa, da, ldda, M, width, w, rs, ws, srs, N, flags & ~OTPU_ACC, k0);
+    a.out = part; a.ors = N;
+    a.q_bs = width; a.sa_bs = M; a.da_bs = width / 32;
+    a.w_bs = fmt == OTPU_INT8 ? width : width / 2; a.ws_bs = 0; a.out_bs = (int64_t)M * N;
+    a.k0_bs = plain ? 0 : width / OTPU_D;
+    rc = launch_gemv(a, fmt, R, s);
+    if (rc) return rc;
+    const int64_t tot = (int64_t)M * N;
+    sum_parts<<<(unsigned)((tot + 255) / 256), 256, 0, s>>>(part, (int64_t)M * N, R, M, N, (flags & OTPU_ACC) != 0,
+                                                            out, ors);
+    return otpu_launch_check("mm_ranges");
 }
 
 extern "C" int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8_t* da, int K, const uint8_t* w,

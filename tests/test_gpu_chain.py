@@ -1,0 +1,182 @@
+"""GPU parity of the chained decode path: QACT over ranges (with the fused VOP MUL), the per-range
+MMs with their ACC chain (otpu_mm_ranges), and the whole Qwen3-shaped decode step
+(opentpu_amd.chain.DecodeChain, eager and as a replayed HIP graph) against oracle/chain.py,
+bit for bit."""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import same_bits
+from oracle import chain as CH
+from oracle import fp32 as F
+from oracle import mm as MM
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def X():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    from opentpu_amd import _lib
+    _lib.load()
+    return _lib
+
+
+def spread(rng, M, K, s=5.0, g=8):
+    return (rng.standard_normal((M, K)) * np.exp(rng.uniform(-s, s, (M, K // g, 1)))
+            .repeat(g, 2).reshape(M, K)).astype(np.float32)
+
+
+@pytest.mark.parametrize("width,mul", [(256, False), (256, True), (384, True), (3072, False), (128, True)])
+def test_qact_ranges(X, width, mul):
+    import torch
+    rng = np.random.default_rng(width + mul)
+    M, K = 3, 3072
+    a = spread(rng, M, 2 * K)                      # [g | u] side by side, like the gate/up output
+    a[1, 5:300] = 0
+    x, u = a[:, :K], a[:, K:]
+    say("qact_ranges", width, mul)
+    ad = torch.from_numpy(a).cuda()
+    R = K // width
+    q = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    S = torch.empty((R * M,), dtype=torch.float32, device="cuda")
+    d = torch.empty((M, K // 32), dtype=torch.uint8, device="cuda")
+    X.call("otpu_qact_ranges", X.ptr(ad), X.ptr(ad[:, K:]) if mul else None, M, K, 2 * K, width, 32, 0,
+           X.ptr(q), K, X.ptr(S), X.ptr(d), K // 32, X.stream())
+    src = F.mul(x, u) if mul else x
+    qh, Sh, dh = q.cpu().numpy(), S.cpu().numpy().reshape(R, M), d.cpu().numpy()
+    for r in range(R):
+        q0, S0, d0 = F.quantize_mx(src[:, r * width:(r + 1) * width], 32)
+        assert np.array_equal(qh[:, r * width:(r + 1) * width], q0)
+        assert same_bits(Sh[r], S0)
+        assert np.array_equal(dh[:, r * width // 32:(r + 1) * width // 32], d0)
+
+
+def _weights(rng, N, K, fmt, rsc=False):
+    from oracle import formats as Q
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    if rsc:
+        return Q.pack_rsc(W)
+    return Q.pack_int8x(W) if fmt == "int8" else Q.pack_x4(W, fmt)
+
+
+@pytest.mark.parametrize("fmt,width,M,acc,rsc", [
+    ("int8", 128, 1, False, False), ("int8", 384, 3, True, False), ("int8", 256, 2, False, True),
+    ("int4", 256, 1, False, False), ("int4", 512, 4, True, False), ("fp4", 256, 2, False, False),
+])
+def test_mm_ranges(X, fmt, width, M, acc, rsc):
+    import torch
+    rng = np.random.default_rng(7 * width + M)
+    K, N = 1536, 200
+    rows, srows = _weights(rng, N, K, fmt, rsc)
+    x = spread(rng, M, K)
+    R = K // width
+    qs, Sas, das = [], [], []
+    for r in range(R):
+        q0, S0, d0 = F.quantize_mx(x[:, r * width:(r + 1) * width], 32, row_mode=rsc)
+        qs.append(q0), Sas.append(S0), das.append(d0)
+    q, Sa, da = np.concatenate(qs, 1), np.stack(Sas), np.concatenate(das, 1)
+    old = rng.standard_normal((M, N)).astype(np.float32)
+    bpb = 128 if fmt == "int8" else 64
+    y = old if acc else None
+    for r in range(R):
+        k0 = 0 if rsc else r * width // 128
+        part = rows[:, r * width // 128 * bpb:(r + 1) * width // 128 * bpb]
+        y = MM.mm(qs[r], Sas[r], das[r], part, srows, fmt, width, k0=k0,
+                  flags=(MM.ACC if y is not None else 0) | (MM.RSC if rsc else 0), old=y)
+    say("mm_ranges", fmt, width, M, acc, rsc)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    qd, Sad, dad, wd, sd = d(q), d(Sa.reshape(-1)), d(da), d(rows), d(srows)
+    out = d(old if acc else np.zeros((M, N), np.float32))
+    part = torch.empty((R, M, N), dtype=torch.float32, device="cuda")
+    fl = (X.ACC if acc else 0) | (X.RSC if rsc else 0)
+    X.call("otpu_mm_ranges", X.ptr(qd), K, X.ptr(Sad), X.ptr(dad), K // 32, M, K, width, X.ptr(wd), rows.shape[1],
+           X.ptr(sd), srows.shape[1], N, X.FMT[fmt], fl, 0, X.ptr(part), X.ptr(out), N, X.stream())
+    assert same_bits(out.cpu().numpy(), y)
+
+
+def test_mm_ranges_refusals(X):
+    import torch
+    from opentpu_amd._lib import OtpuError
+    t = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    p = X.ptr(t)
+    with pytest.raises(OtpuError):      # 4-bit ranges must be whole 128-byte chunks (256 columns)
+        X.call("otpu_mm_ranges", p, 1024, p, p, 32, 1, 1024, 128, p, 512, p, 40, 8, X.FMT["int4"], 0, 0, p, p, 8,
+               X.stream())
+    with pytest.raises(OtpuError):      # ranges must tile K
+        X.call("otpu_mm_ranges", p, 1024, p, p, 32, 1, 1024, 384, p, 1024, p, 12, 8, X.FMT["int8"], 0, 0, p, p, 8,
+               X.stream())
+
+
+def _host_layers(chain):
+    return [{k: (r.cpu().numpy(), s.cpu().numpy()) for k, (r, s) in w.items()} for w in chain.layers]
+
+
+def test_chain_layers_small(X):
+    """Each layer on its own N(0,1) input: every intermediate (qkv, o, gate/up, down) bit-exact."""
+    import torch
+    from opentpu_amd.chain import DecodeChain, Shape
+    sh = Shape(hidden=256, q_dim=512, kv_dim=256, F=768, layers=3)
+    say("chain small: pack")
+    ch = DecodeChain.synthetic(sh, "int4", seed0=7, std=0.05)
+    assert ch.width == CH.down_chunk(768, "int4") == 256
+    host = _host_layers(ch)
+    rng = np.random.default_rng(5)
+    for l in range(sh.layers):
+        x = rng.standard_normal((1, 256)).astype(np.float32)
+        xd = torch.from_numpy(x).cuda()
+        yd = torch.empty((1, 256), dtype=torch.float32, device="cuda")
+        say("chain small: layer", l)
+        ch.layer(l, xd, yd)
+        y0, mid = CH.layer(x, host[l], "int4", 512, 768)
+        assert same_bits(ch.qkv.cpu().numpy(), mid["qkv"])
+        assert same_bits(ch.o.cpu().numpy(), mid["o"])
+        assert same_bits(ch.gu.cpu().numpy(), mid["gu"])
+        assert same_bits(yd.cpu().numpy(), y0)
+    x = rng.standard_normal((1, 256)).astype(np.float32)
+    y = ch.step(x).cpu().numpy()
+    assert same_bits(y, CH.step(x, host, "int4", 512, 768))
+
+
+def test_chain_c4_full_and_graph(X):
+    """The c4 workload (28 layers, Qwen3-0.6B linears, int4x weights seeded 100 + layer): the
+    eager step and three replays of its HIP graph (with eager work between them) all equal the
+    oracle's step bit for bit; the first layers' outputs are not all zero."""
+    import torch
+    from opentpu_amd.chain import DecodeChain, Shape
+    say("chain c4: pack")
+    ch = DecodeChain.synthetic(Shape(), "int4", seed0=100)
+    host = _host_layers(ch)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((1, 1024)).astype(np.float32)
+    say("chain c4: layer by layer")
+    xo, xd = x, torch.from_numpy(x).cuda()
+    nonzero = []
+    for l in range(28):
+        yd = torch.empty((1, 1024), dtype=torch.float32, device="cuda")
+        ch.layer(l, xd, yd)
+        xo, _ = CH.layer(xo, host[l], "int4")
+        assert same_bits(yd.cpu().numpy(), xo), f"layer {l}"
+        nonzero.append(int(np.count_nonzero(xo)))
+        xd = yd
+    say("nonzero outputs per layer", nonzero)
+    assert nonzero[0] > 900
+    want = xo
+    say("chain c4: eager step")
+    assert same_bits(ch.step(x).cpu().numpy(), want)
+    say("chain c4: graph")
+    ch.capture()
+    for i in range(3):
+        xi = rng.standard_normal((1, 1024)).astype(np.float32) if i == 1 else x
+        got = ch.replay(xi).cpu().numpy()
+        exp = want if i != 1 else CH.step(xi, host, "int4")
+        assert same_bits(got, exp), f"replay {i}"
+        torch.cuda.synchronize()
+        ch.qkv.fill_(float(i))                     # eager work between replays
