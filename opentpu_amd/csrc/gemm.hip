@@ -38,6 +38,7 @@ struct GemmArgs {
     const float* alpha;
     float* out; int64_t ors;
     int tiles_m, tiles_n;
+    int vec4;                   // out 16-byte aligned and ors a multiple of 4: float4 stores
 };
 
 // byte offset of 16-byte chunk c of tile row r (rows of 128 bytes, chunks XOR-swizzled)
@@ -69,6 +70,7 @@ struct Smem {
     int8_t (*B)[GBN * GBK];
     uint32_t (*Da)[GBM];
     uint8_t (*Dw)[GBN];
+    int8_t* ring;               // NS stages of A | B (the masked passes use its first 64 KB)
 };
 
 // one K stage of a thread's staged operands: 4 A and 4 B chunks, its row's da word / dw byte
@@ -94,6 +96,106 @@ __device__ __forceinline__ GStage gstage_load(const int8_t* const (&ga)[4], cons
     st.da = (MA && hasDa) ? *reinterpret_cast<const uint32_t*>(gda + 4 * kt) : 0u;
     st.dw = (MB && hasDw) ? (uint32_t)gdw[kt] : 0u;
     return st;
+}
+
+// ---- the single-plane pipeline: a ring of NS K-stages in LDS, filled by direct-to-LDS loads ----
+// A stage is the A and B tiles of 128 rows x RBK bytes; NS - 1 stages are in flight while one
+// is multiplied.  global_load_lds_dwordx4 writes a wave's 64 x 16 bytes to 1 KB of LDS at M0
+// (lane L at M0 + 16 L), so lane L of a wave's instruction fetches the global chunk that belongs
+// at LDS slot L of its 1 KB block: with CPR = RBK / 16 chunks a row, row r = block * (64 / CPR)
+// + L / CPR, stored slot L % CPR, i.e. the row's chunk (L % CPR) ^ rswz(r) (the XOR swizzle
+// that puts the 16 rows a ds_read_b128 fragment reads on distinct banks).
+// The loads are issued from inline assembly and their completion awaited with explicit
+// s_waitcnt vmcnt(n): the compiler's own accounting would wait for every stage in flight.
+#ifndef OTPU_RING_BK
+#define OTPU_RING_BK 128
+#endif
+#ifndef OTPU_RING_NS
+#define OTPU_RING_NS 4
+#endif
+constexpr int RBK = OTPU_RING_BK;               // K bytes a stage
+constexpr int NS = OTPU_RING_NS;                // stages in the ring
+constexpr int CPR = RBK / 16;                   // 16-byte chunks a row
+constexpr int TILE = GBM * RBK;                 // bytes of one operand tile of a stage
+constexpr int STAGE = 2 * TILE;                 // A then B
+constexpr int LPS = 2 * TILE / 1024 / 4;        // direct loads a wave issues per stage
+constexpr int RING = NS * STAGE > 2 * 2 * GBM * GBK ? NS * STAGE : 2 * 2 * GBM * GBK;
+static_assert(RBK == 64 || RBK == 128, "ring stages of 64 or 128 bytes");
+static_assert(NS >= 2 && (NS - 2) * LPS <= 63, "vmcnt holds at most 63");
+
+__device__ __forceinline__ int rswz(int r) { return RBK == 128 ? (r >> 1) & 7 : (r >> 2) & 3; }
+__device__ __forceinline__ int rof(int r, int c) { return r * RBK + ((c ^ rswz(r)) << 4); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ void dma16(const int8_t* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "memory");
+}
+
+// wait until at most n of this wave's direct loads are outstanding
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// wait for stage kt when `ahead` later stages have been issued (ahead <= NS - 2)
+__device__ __forceinline__ void wait_stage(int ahead) {
+    switch (ahead) {
+#define OTPU_WAIT_CASE(x) case x: if constexpr (x <= NS - 2) wait_dma<x * LPS>(); break;
+        OTPU_WAIT_CASE(7) OTPU_WAIT_CASE(6) OTPU_WAIT_CASE(5) OTPU_WAIT_CASE(4)
+        OTPU_WAIT_CASE(3) OTPU_WAIT_CASE(2) OTPU_WAIT_CASE(1)
+#undef OTPU_WAIT_CASE
+        default: wait_dma<0>();
+    }
+}
+
+// LDS reads of the workgroup done, then the barrier (no fence: the direct loads are awaited
+// by each wave before it arrives)
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+
+// this lane's source rows of the ring's direct loads: instruction u of a stage reads row
+// ga[u] (A, u < LPS / 2) or gb[u] (B); rows past M or N read the last valid row
+struct RingSrc {
+    const int8_t* ga[LPS / 2];
+    const int8_t* gb[LPS / 2];
+    uint32_t base;                              // the wave's LDS byte address in stage 0
+};
+
+__device__ __forceinline__ RingSrc ring_src(const GemmArgs& a, const int8_t* ring, int m0, int n0) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    RingSrc rs;
+#pragma unroll
+    for (int u = 0; u < LPS / 2; ++u) {
+        const int blk = w * (LPS / 2) + u;
+        const int r = blk * (64 / CPR) + lane / CPR, c = (lane % CPR) ^ rswz(r);
+        rs.ga[u] = a.q + (int64_t)min(m0 + r, a.M - 1) * a.ldq + 16 * c;
+        rs.gb[u] = a.w + (int64_t)min(n0 + r, a.N - 1) * a.rs + 16 * c;
+    }
+    rs.base = lds_addr(ring) + (uint32_t)(w * (LPS / 2) * 1024);
+    return rs;
+}
+
+__device__ __forceinline__ void ring_issue(const RingSrc& rs, int kt) {
+    const uint32_t sl = rs.base + (uint32_t)((kt % NS) * STAGE);
+    const int o = kt * RBK;
+#pragma unroll
+    for (int u = 0; u < LPS / 2; ++u) dma16(rs.ga[u] + o, sl + 1024u * u);
+#pragma unroll
+    for (int u = 0; u < LPS / 2; ++u) dma16(rs.gb[u] + o, sl + TILE + 1024u * u);
+}
+
+// the first NS - 1 stages (issued before the tile's offsets and constants are known; a tile
+// that turns out not to be single-plane waits for them and reuses the ring's memory)
+__device__ __forceinline__ void ring_prologue(const GemmArgs& a, const int8_t* ring, int m0, int n0) {
+    const RingSrc rs = ring_src(a, ring, m0, n0);
+    const int KS = a.K / RBK;
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s)
+        if (s < KS) ring_issue(rs, s);
 }
 
 // thread t's chunk u is tile row (t + 256 u) >> 3 = (t >> 3) + 32 u, chunk t & 7
@@ -189,11 +291,63 @@ __device__ __forceinline__ void gemm_pass(const GemmArgs& a, const Smem& sm, v4i
     __syncthreads();
 }
 
-// a wave's 64 x 64 outputs: y = (accf * Sw[n]) * (Sa[m] * 2^-16) (accf = i2f of the exact
-// integer), then ACC / ASCALE.  Values are formed first and stored in a burst with no loads in
-// between (the old outputs of ACC / ASCALE are all loaded before any store), so the stores
-// stream instead of waiting on each other.
-__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int m0, int n0, float (&v)[4][4][4],
+// one unmasked plane over all of K through the LDS ring, whose first NS - 1 stages
+// ring_prologue issued.  A stage's fragments are read from LDS up front; its MFMAs are then
+// interleaved with the direct loads that refill the ring (one load every 4 MFMAs), so the
+// matrix pipe and the load path work at the same time (issued in a block, the loads stall the
+// wave behind the loads already in flight before its first MFMA).
+__device__ __forceinline__ void gemm_pass_ring(const GemmArgs& a, int8_t* ring, v4i (&acc)[4][4], int m0, int n0) {
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wid >> 1, wn = wid & 1;
+    const RingSrc rs = ring_src(a, ring, m0, n0);
+    const int KS = a.K / RBK;
+    constexpr int KSTEP = RBK / 64;                       // 64-deep MFMA steps a stage
+    constexpr int EVERY = 16 * KSTEP / LPS;               // MFMAs per refill load
+    for (int kt = 0; kt < KS; ++kt) {
+        wait_stage(min(NS - 2, KS - 1 - kt));            // stage kt landed (this wave's part)
+        ring_barrier();                                  // ... everywhere; stage kt - 1 read
+        const int8_t* A = ring + (kt % NS) * STAGE;
+        const int8_t* B = A + TILE;
+        v4i fa[KSTEP][4], fb[KSTEP][4];
+#pragma unroll
+        for (int ks = 0; ks < KSTEP; ++ks) {
+            const int c = ks * 4 + (lane >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fa[ks][i] = *reinterpret_cast<const v4i*>(A + rof(wm * 64 + i * 16 + (lane & 15), c));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[ks][j] = *reinterpret_cast<const v4i*>(B + rof(wn * 64 + j * 16 + (lane & 15), c));
+        }
+        const int nk = kt + NS - 1;                       // the stage the refill loads fetch
+        const bool refill = nk < KS;
+        const uint32_t sl = rs.base + (uint32_t)((nk % NS) * STAGE);
+        const int o = nk * RBK;
+#pragma unroll
+        for (int ks = 0; ks < KSTEP; ++ks)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+                    const int x = (ks * 16 + i * 4 + j);
+                    if (x % EVERY == EVERY - 1 && refill) {
+                        const int u = x / EVERY;
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (u < LPS / 2) dma16(rs.ga[u] + o, sl + 1024u * u);
+                        else dma16(rs.gb[u - LPS / 2] + o, sl + TILE + 1024u * (u - LPS / 2));
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+    }
+    ring_barrier();
+}
+
+// A full tile leaves through LDS: each wave writes its 64 x 64 values in the MFMA layout (rows
+// 68 floats apart: the 4 row groups of a write land on distinct banks) and reads them back as
+// float4 rows, so every store instruction writes 4 rows x 256 contiguous bytes.  `lds` is the
+// ring's memory (every wave is past its last read of the ring when the epilogue starts).
+constexpr int TPS = 68;                         // transpose row stride, floats
+
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int8_t* lds, int m0, int n0, float (&v)[4][4][4],
                                               const float (&sw)[4], const float (&sa2)[4][4]) {
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int mb = m0 + (wid >> 1) * 64 + 4 * (lane >> 4), nb = n0 + (wid & 1) * 64 + (lane & 15);
@@ -204,6 +358,51 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int m0, int n0,
 #pragma unroll
             for (int t = 0; t < 4; ++t) v[i][j][t] = fmul(fmul(v[i][j][t], sw[j]), sa2[i][t]);
     const bool full = m0 + GBM <= a.M && n0 + GBN <= a.N;
+    if (full && a.vec4) {
+        float* T = reinterpret_cast<float*>(lds) + wid * 64 * TPS;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) T[(16 * i + 4 * (lane >> 4) + t) * TPS + 16 * j + (lane & 15)] = v[i][j][t];
+        const int q = lane & 15, g = lane >> 4;
+        const int mr = m0 + (wid >> 1) * 64 + g, nc = n0 + (wid & 1) * 64 + 4 * q;
+        float4 y[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) y[s] = *reinterpret_cast<const float4*>(T + (g + 4 * s) * TPS + 4 * q);
+        if (a.flags & (OTPU_ACC | OTPU_ASCALE)) {
+            float4 old[16];
+#pragma unroll
+            for (int s = 0; s < 16; ++s) old[s] = *reinterpret_cast<const float4*>(a.out + (int64_t)(mr + 4 * s) * a.ors + nc);
+            const bool asc = (a.flags & OTPU_ASCALE) != 0;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const float al = asc ? a.alpha[mr + 4 * s] : 1.0f;
+                if (asc) {
+                    y[s].x = fadd(fmul(old[s].x, al), y[s].x); y[s].y = fadd(fmul(old[s].y, al), y[s].y);
+                    y[s].z = fadd(fmul(old[s].z, al), y[s].z); y[s].w = fadd(fmul(old[s].w, al), y[s].w);
+                } else {
+                    y[s].x = fadd(old[s].x, y[s].x); y[s].y = fadd(old[s].y, y[s].y);
+                    y[s].z = fadd(old[s].z, y[s].z); y[s].w = fadd(old[s].w, y[s].w);
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            float* p = a.out + (int64_t)(mr + 4 * s) * a.ors + nc;
+#ifndef OTPU_GEMM_NT_STORE
+#define OTPU_GEMM_NT_STORE 1
+#endif
+#if OTPU_GEMM_NT_STORE
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            __builtin_nontemporal_store(f32x4{y[s].x, y[s].y, y[s].z, y[s].w}, reinterpret_cast<f32x4*>(p));
+#else
+            *reinterpret_cast<float4*>(p) = y[s];
+#endif
+        }
+        return;
+    }
     if (a.flags & (OTPU_ACC | OTPU_ASCALE)) {
         float old[4][4][4];
 #pragma unroll
@@ -265,7 +464,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int
         for (int d = 0; d <= s; ++d) {
             const int e = s - d;
             if (!(dmask >> d & 1) || e > 16 || !(emask >> e & 1)) continue;
-            gemm_pass<MA, MB>(a, sm, acc, m0, n0, d, e);
+            if (!MA && !MB) gemm_pass_ring(a, sm.ring, acc, m0, n0);
+            else gemm_pass<MA, MB>(a, sm, acc, m0, n0, d, e);
         }
     }
     // acc = C << (16 - smax) with C an int32: i2f(acc) = rne(C) * 2^(16 - smax), exactly
@@ -276,15 +476,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int t = 0; t < 4; ++t) v[i][j][t] = ldexpf((float)acc[i][j][t], 16 - smax);
-    tile_epilogue(a, m0, n0, v, sw, sa2);
+    tile_epilogue(a, sm.ring, m0, n0, v, sw, sa2);
 }
 
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
-    __shared__ __align__(16) int8_t sA[2][GBM * GBK];
-    __shared__ __align__(16) int8_t sB[2][GBN * GBK];
+    __shared__ __align__(16) int8_t sRing[RING];
     __shared__ uint32_t sDa[2][GBM];       // the stage's four da bytes per activation row
     __shared__ uint8_t sDw[2][GBN];        // the stage's dw byte per weight row
-    __shared__ uint32_t sMask[2];          // d values and e values present in the tile
+    __shared__ uint32_t sMask[8];          // per wave: d values and e values present in the tile
 
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wid >> 1, wn = wid & 1;
@@ -306,10 +505,26 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     const bool plain = unit || (a.flags & OTPU_RSC) != 0;
     const int KT = a.K / GBK;
 
+    // the ring's first stages go out first: their latency overlaps the offset scan and the
+    // epilogue constants (a masked tile waits for them before reusing the ring)
+    ring_prologue(a, sRing, m0, n0);
+
     // the offsets present in this tile: d over its activation rows, e over its weight rows.
     // Two threads a row; the loads of a thread are independent (issued back to back).
-    if (tid < 2) sMask[tid] = 0;
-    __syncthreads();
+    // epilogue constants of this lane's outputs (loaded now, used after the K loop)
+    float sw[4], sa2[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 64 + j * 16 + (lane & 15);
+        sw[j] = (unit || n >= a.N) ? 1.0f : *reinterpret_cast<const float*>(a.ws + (int64_t)n * a.srs);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int m = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + t;
+            sa2[i][t] = m < a.M ? a.Sa[m] : 0.0f;
+        }
     {
         uint32_t dm = 0, em = 0;
         const int r = tid & (GBM - 1), h = tid >> 7;
@@ -340,35 +555,33 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
             em |= __shfl_xor(em, o, 64);
         }
         if (lane == 0) {
-            atomicOr(&sMask[0], dm);
-            atomicOr(&sMask[1], em);
+            sMask[2 * wid] = dm;
+            sMask[2 * wid + 1] = em;
         }
     }
     __syncthreads();
-    const uint32_t dmask = sMask[0] & 0x1FFFFu, emask = sMask[1] & 0x1FFFFu;
+    uint32_t dall = 0, eall = 0;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+        dall |= sMask[2 * x];
+        eall |= sMask[2 * x + 1];
+    }
+    const uint32_t dmask = dall & 0x1FFFFu, emask = eall & 0x1FFFFu;
     // groups beyond the window exist: masking must drop them even with one live plane
-    const bool over = ((sMask[0] | sMask[1]) >> 17) & 1;
+    const bool over = ((dall | eall) >> 17) & 1;
     // the s = d + e values with a live plane, smin and smax
     uint32_t smask = 0;
     for (int d = 0; d <= 16; ++d)
         if (dmask >> d & 1) smask |= (emask << d) & 0x1FFFFu;
 
-    // epilogue constants of this lane's outputs
-    float sw[4], sa2[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 64 + j * 16 + (lane & 15);
-        sw[j] = (unit || n >= a.N) ? 1.0f : *reinterpret_cast<const float*>(a.ws + (int64_t)n * a.srs);
-    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int m = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + t;
-            sa2[i][t] = m < a.M ? fmul(a.Sa[m], pow2f(-16)) : 0.0f;
-        }
+        for (int t = 0; t < 4; ++t) sa2[i][t] = fmul(sa2[i][t], pow2f(-16));
 
     if (smask == 0) {                               // every group drops: acc = 0
+        wait_dma<0>();                              // (the ring prologue's loads end in LDS)
+        ring_barrier();
         float v[4][4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -376,13 +589,14 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int t = 0; t < 4; ++t) v[i][j][t] = 0.0f;
-        tile_epilogue(a, m0, n0, v, sw, sa2);
+        tile_epilogue(a, sRing, m0, n0, v, sw, sa2);
         return;
     }
     const int smin = __builtin_ctz(smask), smax = 31 - __builtin_clz(smask);
     // |acc| <= K * 127^2 * 2^(smax - smin) must stay below 2^31 in the int32 accumulators
     const bool fits = (int64_t)a.K * 16129 <= (((int64_t)1 << 31) - 1) >> (smax - smin);
     if (!fits) {
+        wait_dma<0>();
         for (int idx = tid; idx < GBM * GBN; idx += 256) {
             const int r = idx / GBN, c = idx % GBN;
             const int m = m0 + r, n = n0 + c;
@@ -399,9 +613,15 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
         return;
     }
     const bool single = !over && __builtin_popcount(dmask) == 1 && __builtin_popcount(emask) == 1;
-    const Smem sm{sA, sB, sDa, sDw};
-    if (single) gemm_tile<false, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
-    else if (plain) gemm_tile<true, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
+    const Smem sm{reinterpret_cast<int8_t(*)[GBM * GBK]>(sRing),
+                  reinterpret_cast<int8_t(*)[GBN * GBK]>(sRing + 2 * GBM * GBK), sDa, sDw, sRing};
+    if (single) {
+        gemm_tile<false, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
+        return;
+    }
+    wait_dma<0>();                                  // the masked passes reuse the ring's memory
+    ring_barrier();
+    if (plain) gemm_tile<true, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
     else gemm_tile<true, true>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
 }
 
@@ -422,6 +642,7 @@ int otpu_gemm_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* 
     a.flags = flags; a.k0 = k0; a.alpha = alpha; a.out = out; a.ors = ors;
     a.tiles_m = (M + GBM - 1) / GBM;
     a.tiles_n = (N + GBN - 1) / GBN;
+    a.vec4 = ((uintptr_t)out % 16 == 0) && (ors % 4 == 0);
     gemm_i8_kernel<<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
     return otpu_launch_check("mm gemm");
 }
