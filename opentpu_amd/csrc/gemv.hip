@@ -107,55 +107,123 @@ __device__ __forceinline__ uint32_t piece_scale(const uint8_t* sb, uint32_t ro, 
     return *reinterpret_cast<const uint32_t*>(sb + (ro + (uint32_t)(8 + 4 * (k0 + (p >> 2)))));
 }
 
-// B * c for the piece's group(s); shA = W - da of the piece's 32-group (activation side)
-template <int FMT>
-__device__ __forceinline__ int64_t piece_term(int c0, int c1, uint32_t sc, int shA, int p, bool plain) {
+// B * c for the piece's group(s) as an exact double; shA = W - da of the piece's 32-group
+// (activation side).  |m c| < 2^22 and the shift is at most 16, so every term and every sum
+// of terms of one MM (|acc| < 2^47) is an integer a double holds exactly: the accumulation
+// order cannot change a bit, and cvt_f32_f64 of the sum is i2f's RNE rounding.
+template <int FMT, bool PLAIN>
+__device__ __forceinline__ double piece_term(int c0, int c1, uint32_t sc, int shA, int p) {
     if (FMT == OTPU_INT8) {
-        int sh = shA - (plain ? 0 : (int)sc);
-        return sh >= 0 ? ((int64_t)c0 << sh) : 0;
+        const int sh = shA - (PLAIN ? 0 : (int)sc);
+        return sh >= 0 ? __builtin_ldexp((double)c0, sh) : 0.0;
     }
     if (FMT == OTPU_NVFP4) {
-        int64_t t = 0;
+        double t = 0.0;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            int e4 = (int)((sc >> (8 * h)) & 0xFF), E = (e4 >> 3) & 15, mt = e4 & 7;
-            int m = plain ? 1 : (E ? 8 + mt : mt);
-            int sh = shA - (plain ? 0 : 15 - (E > 1 ? E : 1));
-            t += sh >= 0 ? (int64_t)(m << sh) * (int64_t)(h ? c1 : c0) : 0;
+            const int e4 = (int)((sc >> (8 * h)) & 0xFF), E = (e4 >> 3) & 15, mt = e4 & 7;
+            const int m = PLAIN ? 1 : (E ? 8 + mt : mt);
+            const int sh = shA - (PLAIN ? 0 : 15 - (E > 1 ? E : 1));
+            const int mm = sh >= 0 ? m : 0;
+            t += __builtin_ldexp((double)__mul24(mm, h ? c1 : c0), sh);
         }
         return t;
     }
-    int m = plain ? 1 : (int)((sc >> (8 + 6 * (p & 3))) & 63);
-    int sh = shA - (plain ? 0 : (int)(sc & 0xFF));
-    return sh >= 0 ? (int64_t)(m << sh) * (int64_t)c0 : 0;
+    const int m = PLAIN ? 1 : (int)((sc >> (8 + 6 * (p & 3))) & 63);
+    const int sh = shA - (PLAIN ? 0 : (int)(sc & 0xFF));
+    const int mm = sh >= 0 ? m : 0;
+    return __builtin_ldexp((double)__mul24(mm, c0), sh);
 }
 
-// rows a team takes per iteration: about four 16-byte loads in flight per lane
+// ---- cross-lane exchanges of doubles (64-wide waves) ----
+__device__ __forceinline__ uint2 dbits(double x) { return make_uint2(__double2loint(x), __double2hiint(x)); }
+__device__ __forceinline__ double dfrom(uint32_t lo, uint32_t hi) { return __hiloint2double((int)hi, (int)lo); }
+
+// lanes 0..31 keep a, lanes 32..63 keep b; both halves receive the other half's kept operand
+// and return the sum (v_permlane32_swap exchanges a's upper half with b's lower half)
+__device__ __forceinline__ double swap_add32(double a, double b) {
+    const uint2 x = dbits(a), y = dbits(b);
+    const auto lo = __builtin_amdgcn_permlane32_swap(x.x, y.x, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap(x.y, y.y, false, false);
+    return dfrom(lo[0], hi[0]) + dfrom(lo[1], hi[1]);
+}
+
+// the same for lane bit 4 (rows of 16: v_permlane16_swap exchanges a's odd rows with b's even)
+__device__ __forceinline__ double swap_add16(double a, double b) {
+    const uint2 x = dbits(a), y = dbits(b);
+    const auto lo = __builtin_amdgcn_permlane16_swap(x.x, y.x, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap(x.y, y.y, false, false);
+    return dfrom(lo[0], hi[0]) + dfrom(lo[1], hi[1]);
+}
+
+// x from the partner lane across lane bit o (o <= 8) by DPP: row_ror:8 (bit 3),
+// row_half_mirror (lane i <-> 7 - i: crosses bit 2), quad_perm (bits 1, 0)
+template <int O>
+__device__ __forceinline__ double dpp_partner(double x) {
+    constexpr int CTRL = O == 8 ? 0x128 : O == 4 ? 0x141 : O == 2 ? 0x4E : 0xB1;
+    const uint2 u = dbits(x);
+    return dfrom((uint32_t)__builtin_amdgcn_update_dpp(0, (int)u.x, CTRL, 0xF, 0xF, false),
+                 (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u.y, CTRL, 0xF, 0xF, false));
+}
+
+// one reduce-scatter step across lane bit o: lanes with the bit clear return a + partner's a,
+// lanes with it set b + partner's b
+__device__ __forceinline__ double xchg_add(double a, double b, int o, int lane) {
+    if (o == 32) return swap_add32(a, b);
+    if (o == 16) return swap_add16(a, b);
+    const bool up = (lane & o) != 0;
+    const double keep = up ? b : a, give = up ? a : b;
+    const double recv = o == 8 ? dpp_partner<8>(give) : o == 4 ? dpp_partner<4>(give)
+                      : o == 2 ? dpp_partner<2>(give) : dpp_partner<1>(give);
+    return keep + recv;
+}
+
+// x + the partner's x across lane bit o (a plain reduction step: every lane gets the sum)
+__device__ __forceinline__ double xsum(double x, int o) {
+    if (o == 32) return swap_add32(x, x);
+    if (o == 16) return swap_add16(x, x);
+    return x + (o == 8 ? dpp_partner<8>(x) : o == 4 ? dpp_partner<4>(x) : o == 2 ? dpp_partner<2>(x) : dpp_partner<1>(x));
+}
+
+// rows a team takes per iteration: with one piece a lane, 16 rows' loads in flight per wave for
+// one activation row (measured best on MI355X: 8 gave 3% less, 32 no more), fewer as activation
+// rows add sums to carry (R * MR stays 16)
 #ifndef OTPU_GEMV_R1
-#define OTPU_GEMV_R1 8
+#define OTPU_GEMV_R1 16
 #endif
 #ifndef OTPU_GEMV_NT
 #define OTPU_GEMV_NT 1
 #endif
-constexpr int rows_per_team_rt(int L) { return L >= 4 ? 1 : (L == 1 ? OTPU_GEMV_R1 : 2); }
-template <int L>
-constexpr int rows_per_team() { return rows_per_team_rt(L); }
+#ifndef OTPU_GEMV_R2
+#define OTPU_GEMV_R2 2
+#endif
+#ifndef OTPU_GEMV_R4
+#define OTPU_GEMV_R4 2
+#endif
+constexpr int rows_per_team_rt(int L, int mr) {
+    return L >= 4 ? OTPU_GEMV_R4 : (L == 1 ? OTPU_GEMV_R1 / mr : OTPU_GEMV_R2);
+}
+template <int L, int MR>
+constexpr int rows_per_team() { return rows_per_team_rt(L, MR); }
 
 // activation registers a lane holds: MR rows x L pieces x (4 int8 | 8 split 4-bit) dwords
 // ... and the reduce-scatter needs the R * MR sums of an iteration to fit a team of 16 lanes
 constexpr bool fits_rt(int fmt, int mr, int L) {
-    return mr * L * (fmt == OTPU_INT8 ? 4 : 8) <= 64 && rows_per_team_rt(L) * mr <= 16;
+    return mr * L * (fmt == OTPU_INT8 ? 4 : 8) <= 64 && rows_per_team_rt(L, mr) * mr <= 16;
 }
 template <int FMT, int MR, int L>
 constexpr bool fits() { return fits_rt(FMT, MR, L); }
 
-template <int FMT, int MR, int L>
-__global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
+// the kernel body for a team of T lanes (T a compile-time constant: the exchanges of the
+// reduction are then straight-line code)
+template <int FMT, int MR, int L, int T, bool PLAIN>
+__device__ __forceinline__ void gemv_body(const MMArgs& a) {
     constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
-    constexpr int R = rows_per_team<L>();
+    constexpr int R = rows_per_team<L, MR>();
     constexpr int E = R * MR;                             // sums a lane carries per iteration
+    static_assert(E <= T, "a team holds its E sums after the reduce-scatter");
     const int lane = threadIdx.x & 63;
-    const int T = a.T, NT = 64 / T;                       // lanes per team, teams per wave
+    constexpr int NT = 64 / T;                            // teams per wave
     const int tl = lane & (T - 1), team = lane / T;
     const int b = blockIdx.y;                             // batch problem
     const int8_t* q = a.q + b * a.q_bs;
@@ -165,7 +233,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
     const uint8_t* ws = a.ws + b * a.ws_bs;
     float* out = a.out ? a.out + b * a.out_bs : nullptr;
     const int k0 = a.k0 + b * a.k0_bs;
-    const bool plain = (a.flags & (OTPU_UNIT | OTPU_RSC)) != 0;
+    constexpr bool plain = PLAIN;
     const bool unit = (a.flags & OTPU_UNIT) != 0;
     const int W = window_of(FMT);
     const int P = a.P;
@@ -243,54 +311,53 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
                 st.sc[r][i] = piece_scale<FMT>(sb, soff, k0, pc, plain);
             }
         }
-        st.sw = unit ? 1.0f : *reinterpret_cast<const float*>(sb + (uint32_t)min(er * NT + team, last) * (uint32_t)a.srs);
+        st.sw = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(sb + (uint32_t)min(er * NT + team, last) * (uint32_t)a.srs));
     };
     auto compute = [&](const Stage& st, int n0) {
-        int64_t v[E];
+        double v[E];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
 #pragma unroll
             for (int j = 0; j < MR; ++j) {
-                int64_t acc = 0;
+                double acc = 0.0;
 #pragma unroll
                 for (int i = 0; i < L; ++i) {
                     int c0, c1;
                     piece_dot<FMT>(st.wv[r][i], act[j][i], c0, c1);
-                    acc += piece_term<FMT>(c0, c1, st.sc[r][i], shA[j][i], i * T + tl, plain);
+                    acc += piece_term<FMT, PLAIN>(c0, c1, st.sc[r][i], shA[j][i], i * T + tl);
                 }
                 v[r * MR + j] = acc;
             }
         }
         // reduce-scatter over the team: each step halves the values a lane carries (E - 1
-        // shuffles in all), then plain xor steps finish the sums over the team's T lanes
+        // exchanges in all: permlane swaps across lane bits 5 and 4, DPP below), then plain
+        // steps finish the sums over the team's T lanes
         int o = T >> 1;
 #pragma unroll
         for (int h = E / 2; h >= 1; h >>= 1, o >>= 1) {
-            const bool up = (tl & o) != 0;
 #pragma unroll
-            for (int i = 0; i < h; ++i) {
-                const int64_t keep = up ? v[i + h] : v[i];
-                const int64_t give = up ? v[i] : v[i + h];
-                v[i] = keep + __shfl_xor(give, o, 64);
-            }
+            for (int i = 0; i < h; ++i) v[i] = xchg_add(v[i], v[i + h], o, lane);
         }
-        int64_t tot = v[0];
-        for (; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+        double tot = v[0];
+#pragma unroll
+        for (; o > 0; o >>= 1) tot = xsum(tot, o);
         const int n = n0 + er * NT + team;
         if (epilane && n < a.N && ej < a.M) {
             if (a.acc_out) {
-                a.acc_out[(int64_t)ej * a.N + n] = tot;
+                a.acc_out[(int64_t)ej * a.N + n] = (int64_t)tot;
             } else {
-                float y = fmul(fmul(i2f(tot), st.sw), sa2[ej]);
+                // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw
+                // and the finished Sa * 2^-W need no operand flush
+                float y = fmul_f(fmul_f((float)tot, st.sw), sa2[ej]);
                 if (out) {
                     float* op = out + (int64_t)ej * a.ors + n;
                     if (a.flags & OTPU_ASCALE) y = fadd(fmul(*op, a.alpha[ej]), y);
                     else if (a.flags & OTPU_ACC) y = fadd(*op, y);
                     *op = y;
                 }
-                if (a.flags & OTPU_RMAX) atomicMax(a.rmax_key + ej, fkey(y));
+                if (a.flags & OTPU_RMAX) atomicMax(a.rmax_key + ej, fkey_f(y));
                 if (a.best) {
-                    uint64_t cand = ((uint64_t)fkey(y) << 32) | (uint32_t)~(uint32_t)(a.base + n);
+                    uint64_t cand = ((uint64_t)fkey_f(y) << 32) | (uint32_t)~(uint32_t)(a.base + n);
                     best = cand > best ? cand : best;
                 }
             }
@@ -316,6 +383,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
             if (m) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)m);
         }
     }
+}
+
+template <int FMT, int MR, int L, bool PLAIN>
+__global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
+    if (a.T == 64) gemv_body<FMT, MR, L, 64, PLAIN>(a);
+    else if (a.T == 32) gemv_body<FMT, MR, L, 32, PLAIN>(a);
+    else gemv_body<FMT, MR, L, 16, PLAIN>(a);
 }
 
 // a fill kernel (graph-capture friendly, no memset nodes)
@@ -430,7 +504,7 @@ template <int FMT, int MR, int L>
 static void launch_one(const MMArgs& a, int batch, hipStream_t s) {
     static_assert(fits<FMT, 1, L>(), "one activation row always fits");
     if constexpr (fits<FMT, MR, L>()) {
-        constexpr int R = rows_per_team<L>();
+        constexpr int R = rows_per_team<L, MR>();
         const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
         // about 8 resident workgroups per CU over the whole batch; each wave then streams
         // many row groups (its activation registers are loaded once)
@@ -438,7 +512,10 @@ static void launch_one(const MMArgs& a, int batch, hipStream_t s) {
         int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L) / batch;
         if (cap < 1) cap = 1;
         if (blocks > cap) blocks = cap;
-        gemv_kernel<FMT, MR, L><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+        if (a.flags & (OTPU_UNIT | OTPU_RSC))
+            gemv_kernel<FMT, MR, L, true><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+        else
+            gemv_kernel<FMT, MR, L, false><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
     }
 }
 

@@ -27,6 +27,8 @@ __device__ __forceinline__ float fin(float r) {
     return (r != r) ? bitsf(0x7FC00000u) : r;
 }
 __device__ __forceinline__ float fmul(float a, float b) { return fin(ftz(a) * ftz(b)); }
+// fmul for operands already flushed (a fin() result, a flushed load, an integer's float)
+__device__ __forceinline__ float fmul_f(float a, float b) { return fin(a * b); }
 __device__ __forceinline__ float fadd(float a, float b) { return fin(ftz(a) + ftz(b)); }
 __device__ __forceinline__ float fsub(float a, float b) { return fin(ftz(a) - ftz(b)); }
 __device__ __forceinline__ float pow2f(int d) { return bitsf((uint32_t)(d + 127) << 23); }
@@ -35,6 +37,11 @@ __device__ __forceinline__ float pow2f(int d) { return bitsf((uint32_t)(d + 127)
 // < .. < inf < NaN
 __device__ __forceinline__ uint32_t fkey(float x) {
     uint32_t u = fbits(ftz(x));
+    return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+// fkey of a value already flushed
+__device__ __forceinline__ uint32_t fkey_f(float x) {
+    uint32_t u = fbits(x);
     return (u >> 31) ? ~u : (u | 0x80000000u);
 }
 __device__ __forceinline__ float unkey(uint32_t k) {
