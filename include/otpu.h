@@ -104,6 +104,23 @@ int otpu_mm_ranges(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t*
                    int64_t srs, int N, int fmt, int flags, int k0, float* part, float* out,
                    int64_t ors, otpu_stream_t stream);
 
+/* QACT + MM of one activation row in one launch (the chained decode's linear): quantize the fp32
+ * row as QACT does (fp32.quantize_mx(x, 32), opentpu/fp32.py:321-343) and run the MM on it
+ * (opentpu/isasim.py:749-910), in K / width ranges each with its own QACT, as
+ * otpu_qact_ranges + otpu_mm_ranges do without their ACC fold: range r writes its MM output
+ * row to out + r * part_stride (one range: out).  The row quantized is x[0..K) folded with
+ * nsum - 1 more rows sum_stride apart in order (x_0 + x_1 + ..: the ACC chain of a previous
+ * per-range MM, opentpu/isasim.py:899-905), times xmul when given (VOP MUL).  No ACC / ASCALE /
+ * RMAX; width at most 4096, a multiple of 128 (int8) or 256 (4-bit); nsum at most 16. */
+int otpu_mm_qin(const float* x, const float* xmul, int nsum, int64_t sum_stride, int K, int width,
+                const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
+                int k0, float* out, int64_t ors, int64_t part_stride, otpu_stream_t stream);
+
+/* The ACC fold of R rows of n (opentpu/isasim.py:899-905 applied in order): out = add(..add(
+ * add(old | p_0, p_1)..), p_R-1) with FTZ adds, rows pstride apart; old may be NULL. */
+int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float* old, float* out,
+                  otpu_stream_t stream);
+
 /* B independent MMs of one shape in one launch (a layer stack's or an expert set's decode
  * GEMVs): problem b's operands start at the given pointers plus b times the *_bstride
  * (elements of each pointer's type; bytes for w and ws).  No ACC / ASCALE / RMAX. */

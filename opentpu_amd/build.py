@@ -28,18 +28,35 @@ def sources():
 
 
 def build(verbose: bool = True) -> str:
+    """Compile every source to an object in parallel (one hipcc per file), then link."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB + ".tmp"
-    cmd = [hipcc, *FLAGS, "-I", os.path.join(HERE, "..", "include"), *sources(), "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed")
-    warn = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
+    inc = ["-I", os.path.join(HERE, "..", "include")]
+    cflags = [f for f in FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="otpu_build_") as tmpd:
+        def compile_one(src):
+            obj = os.path.join(tmpd, os.path.basename(src) + ".o")
+            cmd = [hipcc, *cflags, *inc, "-c", src, "-o", obj]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            return obj, subprocess.run(cmd, capture_output=True, text=True)
+        with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+            results = list(ex.map(compile_one, sources()))
+        warn = []
+        for obj, r in results:
+            if r.returncode != 0:
+                sys.stderr.write(r.stdout + r.stderr)
+                raise RuntimeError(f"hipcc failed on {obj}")
+            warn += [l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip()]
+        tmp = LIB + ".tmp"
+        cmd = [hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *[o for o, _ in results], "-o", tmp]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise RuntimeError("link failed")
     if verbose and warn:
-        print(warn)
+        print("\n".join(warn))
     os.replace(tmp, LIB)
     return LIB
 

@@ -58,14 +58,21 @@ class Shape:
 
 
 class DecodeChain:
-    """`layers`: per layer a dict name -> (rows, srows) device tensors (uint8)."""
+    """`layers`: per layer a dict name -> (rows, srows) device tensors (uint8).
 
-    KERNELS_PER_LAYER = 9          # 3 QACT, 3 MM, QACT ranges, per-range MM + its ACC chain
+    fused (default): a layer is four kernels, each linear an otpu_mm_qin (the QACT of its input
+    row in the GEMV's prologue); the down projection's per-chunk outputs stay partial and the
+    next layer's prologue folds them in chunk order (the ACC chain), the step's last fold is one
+    otpu_acc_rows.  Unfused: the nine kernels of `layer` (QACT, MM, .. one call each)."""
 
-    def __init__(self, layers: list, shape: Shape = Shape(), fmt: str = "int4"):
+    KERNELS_PER_LAYER = 9          # unfused: 3 QACT, 3 MM, QACT ranges, per-range MM + its ACC fold
+    FUSED_KERNELS_PER_LAYER = 4    # fused: one QACT + MM kernel per linear
+
+    def __init__(self, layers: list, shape: Shape = Shape(), fmt: str = "int4", fused: bool = True):
         self.layers = layers
         self.shape = shape
         self.fmt = fmt
+        self.fused = fused
         s = shape
         self.width = down_chunk(s.F, fmt)
         self.R = s.F // self.width
@@ -84,10 +91,12 @@ class DecodeChain:
         self.Sa = T.empty((self.R,), dtype=f32, device=dev)
         self.da = T.empty((1, kmax // 32), dtype=u8, device=dev)
         self.part = T.empty((self.R, s.hidden), dtype=f32, device=dev)
+        self.parts = [T.zeros((self.R, s.hidden), dtype=f32, device=dev) for _ in range(2)]
         self._graph = None
 
     @staticmethod
-    def synthetic(shape: Shape = Shape(), fmt: str = "int4", seed0: int = 100, std: float = 0.02) -> "DecodeChain":
+    def synthetic(shape: Shape = Shape(), fmt: str = "int4", seed0: int = 100, std: float = 0.02,
+                  fused: bool = True) -> "DecodeChain":
         """Random-init weights N(0, std), layer l from a generator seeded seed0 + l (the weights
         of each linear drawn in the order q, k, v, o, gate, up, down), packed on the GPU."""
         T = X.torch()
@@ -105,16 +114,16 @@ class DecodeChain:
             layers.append({"qkv": quantize_mxu(T.cat([Wq, Wk, Wv]), fmt), "o": quantize_mxu(Wo, fmt),
                            "gu": quantize_mxu(T.cat([Wg, Wu]), fmt), "down": quantize_mxu(Wd, fmt)})
             del Wq, Wk, Wv, Wo, Wg, Wu, Wd
-        return DecodeChain(layers, shape, fmt)
+        return DecodeChain(layers, shape, fmt, fused)
 
     @staticmethod
-    def from_packed(layers: list, shape: Shape = Shape(), fmt: str = "int4") -> "DecodeChain":
+    def from_packed(layers: list, shape: Shape = Shape(), fmt: str = "int4", fused: bool = True) -> "DecodeChain":
         """Packed (rows, srows) pairs per layer (numpy or tensors), e.g. the reference's
         quantize_mxu output, loaded unchanged."""
         out = []
         for wts in layers:
             out.append({k: (X.dev(r, np.uint8), X.dev(sr, np.uint8)) for k, (r, sr) in wts.items()})
-        return DecodeChain(out, shape, fmt)
+        return DecodeChain(out, shape, fmt, fused)
 
     # --- the kernels of one step ---------------------------------------------------------
     def _qact(self, x, K: int) -> None:
@@ -144,8 +153,33 @@ class DecodeChain:
                self.da.shape[1], 1, s.F, self.width, X.ptr(rows), rows.shape[1], X.ptr(srows), srows.shape[1],
                rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(self.part), X.ptr(y), y.shape[1], X.stream())
 
+    def _qin(self, w, x, K: int, width: int, out, part_stride: int = 0, xmul=None, nsum: int = 1,
+             sum_stride: int = 0) -> None:
+        rows, srows = w
+        X.call("otpu_mm_qin", X.ptr(x), X.ptr(xmul), nsum, sum_stride, K, width, X.ptr(rows), rows.shape[1],
+               X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(out), rows.shape[0],
+               part_stride, X.stream())
+
+    def layer_fused(self, l: int, x, nsum: int, parts) -> None:
+        """Queue layer l fused: input = the in-order fold of the nsum rows of x ([nsum, hidden]);
+        output = the down projection's per-chunk rows in parts ([R, hidden], not yet folded)."""
+        s, w = self.shape, self.layers[l]
+        self._qin(w["qkv"], x, s.hidden, s.hidden, self.qkv, nsum=nsum, sum_stride=s.hidden)
+        self._qin(w["o"], self.qkv, s.q_dim, s.q_dim, self.o)
+        self._qin(w["gu"], self.o, s.hidden, s.hidden, self.gu)
+        self._qin(w["down"], self.gu, s.F, self.width, parts, part_stride=s.hidden, xmul=self.gu[:, s.F:])
+
     def _queue(self) -> None:
         n = len(self.layers)
+        if self.fused:
+            src, nsum = self.x, 1
+            for l in range(n):
+                dst = self.parts[l % 2]
+                self.layer_fused(l, src, nsum, dst)
+                src, nsum = dst, self.R
+            X.call("otpu_acc_rows", X.ptr(src), self.R, self.shape.hidden, self.shape.hidden, None, X.ptr(self.y),
+                   X.stream())
+            return
         src = self.x
         for l in range(n):                                # outputs alternate so the last is self.y
             dst = self.y if (n - 1 - l) % 2 == 0 else self.y2

@@ -1,0 +1,77 @@
+// Shared by the decode GEMV sources: the argument block of one MM launch, the register-
+// tiling constants (also used on the host to pick a launch shape) and the per-format launchers,
+// each instantiated in its own translation unit (gemv_int8.hip, gemv_int4.hip, gemv_fp4.hip,
+// gemv_nvfp4.hip) so the four compile in parallel.
+#pragma once
+#include "otpu_common.h"
+
+namespace otpu {
+
+constexpr int LMAX = 8;            // pieces per lane held in registers (K <= 128 * LMAX * 16 / elements)
+
+struct MMArgs {
+    const int8_t* q; int64_t ldq;
+    const float* Sa;
+    const uint8_t* da; int64_t ldda;
+    int M, K;
+    const uint8_t* w; int64_t rs;
+    const uint8_t* ws; int64_t srs;
+    int N, flags, k0;
+    const float* alpha;
+    float* out; int64_t ors;
+    uint32_t* rmax_key;            // RMAX: total-order keys, finished by rmax_finish
+    int64_t* acc_out;              // exact accumulators instead of the epilogue
+    uint64_t* best;                // LM head: max of (key << 32 | ~index)
+    int64_t base;                  // LM head: index of row 0
+    int P, T;                      // 16-byte pieces per row, lanes per row (team)
+    // batch strides (elements of each pointer's type; bytes for w / ws; blocks for k0)
+    int64_t q_bs, sa_bs, da_bs, w_bs, ws_bs, out_bs;
+    int k0_bs;
+    // QACT in the prologue (one activation row): the fp32 row xin (problem b at + b * xin_bs),
+    // the fold of nsum rows sum_stride apart, times xmul when given
+    const float* xin;
+    const float* xmul;
+    int nsum;
+    int64_t sum_stride, xin_bs;
+};
+
+constexpr int QIN_KMAX = 4096;     // columns a prologue QACT holds in LDS
+constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds
+
+// rows a team takes per iteration: with one piece a lane, 16 rows' loads in flight per wave for
+// one activation row (measured best on MI355X: 8 gave 3% less, 32 no more), fewer as activation
+// rows add sums to carry (R * MR stays 16)
+#ifndef OTPU_GEMV_R1
+#define OTPU_GEMV_R1 16
+#endif
+#ifndef OTPU_GEMV_NT
+#define OTPU_GEMV_NT 1
+#endif
+#ifndef OTPU_GEMV_R2
+#define OTPU_GEMV_R2 2
+#endif
+#ifndef OTPU_GEMV_R4
+#define OTPU_GEMV_R4 2
+#endif
+constexpr int rows_per_team_rt(int L, int mr) {
+    return L >= 4 ? OTPU_GEMV_R4 : (L == 1 ? OTPU_GEMV_R1 / mr : OTPU_GEMV_R2);
+}
+template <int L, int MR>
+constexpr int rows_per_team() { return rows_per_team_rt(L, MR); }
+
+// activation registers a lane holds: MR rows x L pieces x (4 int8 | 8 split 4-bit) dwords
+// ... and the reduce-scatter needs the R * MR sums of an iteration to fit a team of 16 lanes
+constexpr bool fits_rt(int fmt, int mr, int L) {
+    return mr * L * (fmt == OTPU_INT8 ? 4 : 8) <= 64 && rows_per_team_rt(L, mr) * mr <= 16;
+}
+template <int FMT, int MR, int L>
+constexpr bool fits() { return fits_rt(FMT, MR, L); }
+
+// launch the streaming GEMV for MR <= 4 activation rows, L pieces a lane (team size a.T)
+template <int FMT>
+void launch_fmt(const MMArgs& a, int mr, int L, int batch, hipStream_t s);
+// launch the GEMV with the QACT of its activation row in the prologue
+template <int FMT>
+void launch_qin_fmt(const MMArgs& a, int L, int batch, hipStream_t s);
+
+}  // namespace otpu

@@ -1,0 +1,546 @@
+// MM for few activation rows (decode GEMV, M <= 4 per launch): the weight-streaming kernel,
+// the LM head with the greedy argmax fused into its epilogue, and VOP ARGMAX.
+// Semantics: opentpu/isasim.py:706-910 (MM), :1141-1152 (ARGMAX), docs/isa.md:226-305.
+//
+// Layout of the work.  A weight row is cut into 16-byte pieces (int8: 16 elements, half a
+// 32-group; 4-bit: 32 elements, one 32-group).  A wave owns R weight rows at a time and lane l
+// takes pieces l, l+64, l+128, .. of each (L = ceil(pieces/64) per lane), so every load is a
+// 16-byte global_load_dwordx4 and a wave's load covers 1 KB of one row.  The activation pieces
+// a lane needs are the same for every row: they are loaded once, into registers (4-bit: split
+// into even / odd element bytes to meet the nibbles).  Per piece:
+//   int8   c = 4 x v_dot4_i32_i8
+//   int4   c = 8 x v_dot4 on (nibble << 4) bytes, then >> 4 (exact)
+//   fp4    E2M1 codes through two v_perm_b32 tables and a sign select, then 8 x v_dot4
+// then B = m << (W - dw - da) (0 where the shift is negative) and an int64 multiply-add.  The
+// wave reduces each row's int64 partials with shuffles and R*M lanes run the fp32 epilogue
+// (three FTZ products) and store.  Scale rows are read per lane piece (4 lanes share a word).
+#pragma once
+#include <cstdlib>
+
+#include "gemv_args.h"
+
+namespace otpu {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// a streamed 16-byte weight load, marked non-temporal (the rows are read once)
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) {
+#if OTPU_GEMV_NT
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
+// E2M1 codes (4 per dword, one per byte, 0..15) -> signed int8 values, twice the E2M1 value
+__device__ __forceinline__ uint32_t dec_e2m1(uint32_t nib) {
+    uint32_t sel = nib & 0x07070707u;
+    uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel);
+    uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, sel);
+    uint32_t msk = ((nib >> 3) & 0x01010101u) * 0xFFu;
+    return (neg & msk) | (pos & ~msk);
+}
+
+// piece sums: int8 (one partial 16-group of a 32-group), 4-bit (c0: whole 32-group, or with
+// nvfp4 the two 16-groups c0 and c1)
+template <int FMT>
+__device__ __forceinline__ void piece_dot(const uint4 wv, const uint32_t* a, int& c0, int& c1) {
+    if (FMT == OTPU_INT8) {
+        int c = __builtin_amdgcn_sdot4((int)wv.x, (int)a[0], 0, false);
+        c = __builtin_amdgcn_sdot4((int)wv.y, (int)a[1], c, false);
+        c = __builtin_amdgcn_sdot4((int)wv.z, (int)a[2], c, false);
+        c0 = __builtin_amdgcn_sdot4((int)wv.w, (int)a[3], c, false);
+        c1 = 0;
+    } else if (FMT == OTPU_INT4) {
+        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        int c = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            c = __builtin_amdgcn_sdot4((int)((wd[t] << 4) & 0xF0F0F0F0u), (int)a[2 * t], c, false);
+            c = __builtin_amdgcn_sdot4((int)(wd[t] & 0xF0F0F0F0u), (int)a[2 * t + 1], c, false);
+        }
+        c0 = c >> 4;
+        c1 = 0;
+    } else {
+        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        int c[2] = {0, 0};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t ev = dec_e2m1(wd[t] & 0x0F0F0F0Fu), od = dec_e2m1((wd[t] >> 4) & 0x0F0F0F0Fu);
+            c[t >> 1] = __builtin_amdgcn_sdot4((int)ev, (int)a[2 * t], c[t >> 1], false);
+            c[t >> 1] = __builtin_amdgcn_sdot4((int)od, (int)a[2 * t + 1], c[t >> 1], false);
+        }
+        if (FMT == OTPU_NVFP4) { c0 = c[0]; c1 = c[1]; }
+        else { c0 = c[0] + c[1]; c1 = 0; }
+    }
+}
+
+// the scale data a piece needs, from the scale row at byte offset ro of base sb (UNIT / RSC: none)
+template <int FMT>
+__device__ __forceinline__ uint32_t piece_scale(const uint8_t* sb, uint32_t ro, int k0, int p, bool plain) {
+    if (plain) return 0;
+    if (FMT == OTPU_INT8) return sb[ro + (uint32_t)(4 + k0 + (p >> 3))];
+    if (FMT == OTPU_NVFP4)
+        return *reinterpret_cast<const uint16_t*>(sb + (ro + (uint32_t)(16 + 8 * (k0 + (p >> 2)) + 2 * (p & 3))));
+    return *reinterpret_cast<const uint32_t*>(sb + (ro + (uint32_t)(8 + 4 * (k0 + (p >> 2)))));
+}
+
+// B * c for the piece's group(s) as an exact double; shA = W - da of the piece's 32-group
+// (activation side).  |m c| < 2^22 and the shift is at most 16, so every term and every sum
+// of terms of one MM (|acc| < 2^47) is an integer a double holds exactly: the accumulation
+// order cannot change a bit, and cvt_f32_f64 of the sum is i2f's RNE rounding.
+template <int FMT, bool PLAIN>
+__device__ __forceinline__ double piece_term(int c0, int c1, uint32_t sc, int shA, int p) {
+    if (FMT == OTPU_INT8) {
+        const int sh = shA - (PLAIN ? 0 : (int)sc);
+        return sh >= 0 ? __builtin_ldexp((double)c0, sh) : 0.0;
+    }
+    if (FMT == OTPU_NVFP4) {
+        double t = 0.0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int e4 = (int)((sc >> (8 * h)) & 0xFF), E = (e4 >> 3) & 15, mt = e4 & 7;
+            const int m = PLAIN ? 1 : (E ? 8 + mt : mt);
+            const int sh = shA - (PLAIN ? 0 : 15 - (E > 1 ? E : 1));
+            const int mm = sh >= 0 ? m : 0;
+            t += __builtin_ldexp((double)__mul24(mm, h ? c1 : c0), sh);
+        }
+        return t;
+    }
+    const int m = PLAIN ? 1 : (int)((sc >> (8 + 6 * (p & 3))) & 63);
+    const int sh = shA - (PLAIN ? 0 : (int)(sc & 0xFF));
+    const int mm = sh >= 0 ? m : 0;
+    return __builtin_ldexp((double)__mul24(mm, c0), sh);
+}
+
+// ---- cross-lane exchanges of doubles (64-wide waves) ----
+__device__ __forceinline__ uint2 dbits(double x) { return make_uint2(__double2loint(x), __double2hiint(x)); }
+__device__ __forceinline__ double dfrom(uint32_t lo, uint32_t hi) { return __hiloint2double((int)hi, (int)lo); }
+
+// lanes 0..31 keep a, lanes 32..63 keep b; both halves receive the other half's kept operand
+// and return the sum (v_permlane32_swap exchanges a's upper half with b's lower half)
+__device__ __forceinline__ double swap_add32(double a, double b) {
+    const uint2 x = dbits(a), y = dbits(b);
+    const auto lo = __builtin_amdgcn_permlane32_swap(x.x, y.x, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap(x.y, y.y, false, false);
+    return dfrom(lo[0], hi[0]) + dfrom(lo[1], hi[1]);
+}
+
+// the same for lane bit 4 (rows of 16: v_permlane16_swap exchanges a's odd rows with b's even)
+__device__ __forceinline__ double swap_add16(double a, double b) {
+    const uint2 x = dbits(a), y = dbits(b);
+    const auto lo = __builtin_amdgcn_permlane16_swap(x.x, y.x, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap(x.y, y.y, false, false);
+    return dfrom(lo[0], hi[0]) + dfrom(lo[1], hi[1]);
+}
+
+// x from the partner lane across lane bit o (o <= 8) by DPP: row_ror:8 (bit 3),
+// row_half_mirror (lane i <-> 7 - i: crosses bit 2), quad_perm (bits 1, 0)
+template <int O>
+__device__ __forceinline__ double dpp_partner(double x) {
+    constexpr int CTRL = O == 8 ? 0x128 : O == 4 ? 0x141 : O == 2 ? 0x4E : 0xB1;
+    const uint2 u = dbits(x);
+    return dfrom((uint32_t)__builtin_amdgcn_update_dpp(0, (int)u.x, CTRL, 0xF, 0xF, false),
+                 (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u.y, CTRL, 0xF, 0xF, false));
+}
+
+// one reduce-scatter step across lane bit o: lanes with the bit clear return a + partner's a,
+// lanes with it set b + partner's b
+__device__ __forceinline__ double xchg_add(double a, double b, int o, int lane) {
+    if (o == 32) return swap_add32(a, b);
+    if (o == 16) return swap_add16(a, b);
+    const bool up = (lane & o) != 0;
+    const double keep = up ? b : a, give = up ? a : b;
+    const double recv = o == 8 ? dpp_partner<8>(give) : o == 4 ? dpp_partner<4>(give)
+                      : o == 2 ? dpp_partner<2>(give) : dpp_partner<1>(give);
+    return keep + recv;
+}
+
+// x + the partner's x across lane bit o (a plain reduction step: every lane gets the sum)
+__device__ __forceinline__ double xsum(double x, int o) {
+    if (o == 32) return swap_add32(x, x);
+    if (o == 16) return swap_add16(x, x);
+    return x + (o == 8 ? dpp_partner<8>(x) : o == 4 ? dpp_partner<4>(x) : o == 2 ? dpp_partner<2>(x) : dpp_partner<1>(x));
+}
+
+// QACT of the problem's fp32 row in the prologue (fp32.quantize_mx(x, 32) of one row, as
+// qact_kernel computes it), once per workgroup: each thread takes float4 chunks of the row
+// (folding nsum partial rows in order, times xmul when given), the workgroup finds the row
+// maximum, each 32-group's 8 threads its group maximum (xor exchanges), and the quantized
+// bytes and group offsets go to LDS; then every lane reads its own pieces (4-bit layouts:
+// even / odd elements split, as the loaded path permutes them).
+template <int FMT, int L, int T>
+__device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&act)[L][FMT == OTPU_INT8 ? 4 : 8],
+                                             int (&shA)[L], float& sa2) {
+    __shared__ __align__(16) uint32_t qs[QIN_KMAX / 4];
+    __shared__ uint8_t ds[QIN_KMAX / 32];
+    __shared__ uint32_t red[4];
+    constexpr int CPT = QIN_KMAX / 4 / 256;            // float4 chunks a thread holds at most
+    const int K = a.K, NC = K >> 2, W = window_of(FMT);
+    const int tid = threadIdx.x;
+    const float* x = a.xin + b * a.xin_bs;
+    const float* xm = a.xmul ? a.xmul + b * a.xin_bs : nullptr;
+    float4 v[CPT];
+    uint32_t m = 0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        const int c = tid + 256 * k;
+        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < NC) {
+            float4 u[QIN_NSUM_MAX];                      // every partial row's chunk in flight
+#pragma unroll
+            for (int s = 0; s < QIN_NSUM_MAX; ++s)
+                if (s < a.nsum) u[s] = reinterpret_cast<const float4*>(x + s * a.sum_stride)[c];
+            float4 t = u[0];
+#pragma unroll
+            for (int s = 1; s < QIN_NSUM_MAX; ++s)       // the ACC fold, in order
+                if (s < a.nsum) {
+                    t.x = fadd(t.x, u[s].x); t.y = fadd(t.y, u[s].y); t.z = fadd(t.z, u[s].z); t.w = fadd(t.w, u[s].w);
+                }
+            if (xm) {                                    // VOP MUL
+                const float4 g = reinterpret_cast<const float4*>(xm)[c];
+                t.x = fmul(t.x, g.x); t.y = fmul(t.y, g.y); t.z = fmul(t.z, g.z); t.w = fmul(t.w, g.w);
+            }
+            t.x = ftz(t.x); t.y = ftz(t.y); t.z = ftz(t.z); t.w = ftz(t.w);
+            v[k] = t;
+            m = max(m, max(max(fbits(t.x) & 0x7FFFFFFFu, fbits(t.y) & 0x7FFFFFFFu),
+                           max(fbits(t.z) & 0x7FFFFFFFu, fbits(t.w) & 0x7FFFFFFFu)));
+        }
+    }
+    m = wave_max_u32(m, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const uint32_t amax = max(max(red[0], red[1]), max(red[2], red[3]));
+    const float fa = bitsf(amax);
+    const float inv = amax ? fmul(127.0f, recip(fa)) : 0.0f;
+    sa2 = fmul(amax ? fmul(fa, bitsf(0x3C010204u)) : 0.0f, pow2f(-W));
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        const int c = tid + 256 * k;
+        if (k * 256 >= NC) break;                        // uniform: the shuffles below converge
+        uint32_t gm = max(max(fbits(v[k].x) & 0x7FFFFFFFu, fbits(v[k].y) & 0x7FFFFFFFu),
+                          max(fbits(v[k].z) & 0x7FFFFFFFu, fbits(v[k].w) & 0x7FFFFFFFu));
+        gm = wave_max_u32(gm, 8);                        // the 8 chunks of this 32-group
+        int dg = 0;
+        if (gm) {
+            dg = (int)(amax >> 23) - (int)(gm >> 23) - ((gm & 0x7FFFFFu) > (amax & 0x7FFFFFu));
+            dg = dg < 0 ? 0 : (dg > 31 ? 31 : dg);
+        }
+        if (c < NC) {
+            const float sc = fmul(inv, pow2f(dg));
+            qs[c] = (uint32_t)(q8(fmul(v[k].x, sc)) & 0xFF) | ((uint32_t)(q8(fmul(v[k].y, sc)) & 0xFF) << 8)
+                  | ((uint32_t)(q8(fmul(v[k].z, sc)) & 0xFF) << 16) | ((uint32_t)(q8(fmul(v[k].w, sc)) & 0xFF) << 24);
+            if ((c & 7) == 0) ds[c >> 3] = (uint8_t)dg;
+        }
+    }
+    __syncthreads();
+    const int tl = tid & (T - 1);
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+        const int p = i * T + tl;
+        const bool ok = p < a.P;
+        if (FMT == OTPU_INT8) {
+            const uint4 q4 = ok ? reinterpret_cast<const uint4*>(qs)[p] : make_uint4(0, 0, 0, 0);
+            act[i][0] = q4.x; act[i][1] = q4.y; act[i][2] = q4.z; act[i][3] = q4.w;
+            shA[i] = W - (ok ? (int)ds[p >> 1] : 0);
+        } else {
+            uint4 v0 = make_uint4(0, 0, 0, 0), v1 = v0;
+            if (ok) {
+                v0 = reinterpret_cast<const uint4*>(qs)[2 * p];
+                v1 = reinterpret_cast<const uint4*>(qs)[2 * p + 1];
+            }
+            const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                act[i][2 * t] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x06040200u);
+                act[i][2 * t + 1] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x07050301u);
+            }
+            shA[i] = W - (ok ? (int)ds[p] : 0);
+        }
+    }
+}
+
+// the kernel body for a team of T lanes (T a compile-time constant: the exchanges of the
+// reduction are then straight-line code); QIN: the activation row is quantized in the prologue
+template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN = false>
+__device__ __forceinline__ void gemv_body(const MMArgs& a) {
+    constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
+    constexpr int R = rows_per_team<L, MR>();
+    constexpr int E = R * MR;                             // sums a lane carries per iteration
+    static_assert(E <= T, "a team holds its E sums after the reduce-scatter");
+    const int lane = threadIdx.x & 63;
+    constexpr int NT = 64 / T;                            // teams per wave
+    const int tl = lane & (T - 1), team = lane / T;
+    const int b = blockIdx.y;                             // batch problem
+    const int8_t* q = a.q + b * a.q_bs;
+    const float* Sa = a.Sa ? a.Sa + b * a.sa_bs : nullptr;
+    const uint8_t* da = a.da + b * a.da_bs;
+    const uint8_t* w = a.w + b * a.w_bs;
+    const uint8_t* ws = a.ws + b * a.ws_bs;
+    float* out = a.out ? a.out + b * a.out_bs : nullptr;
+    const int k0 = a.k0 + b * a.k0_bs;
+    constexpr bool plain = PLAIN;
+    const bool unit = (a.flags & OTPU_UNIT) != 0;
+    const int W = window_of(FMT);
+    const int P = a.P;
+
+    // activation pieces tl, tl + T, .. and their W - da, per act row, in registers
+    uint32_t act[MR][L][AW];
+    int shA[MR][L];
+    float sa2[MR];
+    if constexpr (QIN) {
+        static_assert(MR == 1, "the prologue QACT quantizes one activation row");
+        // (quantized by qin_prologue below, once the first rows' loads are in flight)
+    } else {
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+            const int p = i * T + tl;
+            const bool ok = p < P && j < a.M;
+            if (FMT == OTPU_INT8) {
+                uint4 v = ok ? *reinterpret_cast<const uint4*>(q + j * a.ldq + 16 * p) : make_uint4(0, 0, 0, 0);
+                act[j][i][0] = v.x; act[j][i][1] = v.y; act[j][i][2] = v.z; act[j][i][3] = v.w;
+                shA[j][i] = W - (ok ? (int)da[j * a.ldda + (p >> 1)] : 0);
+            } else {
+                uint4 v0 = make_uint4(0, 0, 0, 0), v1 = v0;
+                if (ok) {
+                    v0 = *reinterpret_cast<const uint4*>(q + j * a.ldq + 32 * p);
+                    v1 = *reinterpret_cast<const uint4*>(q + j * a.ldq + 32 * p + 16);
+                }
+                const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    act[j][i][2 * t] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x06040200u);
+                    act[j][i][2 * t + 1] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x07050301u);
+                }
+                shA[j][i] = W - (ok ? (int)da[j * a.ldda + p] : 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MR; ++j) sa2[j] = (j < a.M && !a.acc_out) ? fmul(Sa[j], pow2f(-W)) : 0.0f;
+    }
+
+    // wave-uniform by construction; readfirstlane tells the compiler (scalar loop, no exec masks)
+    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    const int RW = R * NT;                      // rows a wave takes per iteration
+    const int stride = nwaves * RW;
+    uint64_t best = 0;
+    // After the reduce-scatter below, value e = r * MR + j of a team sits in the lanes
+    // tl = e * (T / E) .. (e + 1) * (T / E) - 1; the first of them runs its epilogue.
+    const int span = T / E;
+    const int ee = tl / span;
+    const int er = ee / MR, ej = ee % MR;
+    const bool epilane = (tl % span) == 0;
+
+    // one iteration's operands: weight pieces, their scale data, the epilogue row's Sw
+    struct Stage {
+        uint4 wv[R][L];
+        uint32_t sc[R][L];
+        float sw;
+    };
+    // operand addresses: a wave-uniform row-group base (scalar registers) plus 32-bit lane
+    // offsets, so the loads take the saddr + voffset form; rows past N read the last row and
+    // pieces past P the last piece (no branch around a load): the former reach no epilogue, the
+    // latter meet zero activation registers
+    auto load = [&](Stage& st, int n0) {
+        const uint8_t* wb = w + (int64_t)n0 * a.rs;
+        const uint8_t* sb = ws + (int64_t)n0 * a.srs;
+        const int last = a.N - 1 - n0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int dn = min(r * NT + team, last);
+            const uint32_t roff = (uint32_t)dn * (uint32_t)a.rs;
+            const uint32_t soff = (uint32_t)dn * (uint32_t)a.srs;
+#pragma unroll
+            for (int i = 0; i < L; ++i) {
+                const int p = i * T + tl;
+                const int pc = p < P ? p : P - 1;
+                st.wv[r][i] = ld16(wb + (roff + 16u * (uint32_t)pc));
+                st.sc[r][i] = piece_scale<FMT>(sb, soff, k0, pc, plain);
+            }
+        }
+        st.sw = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(sb + (uint32_t)min(er * NT + team, last) * (uint32_t)a.srs));
+    };
+    auto compute = [&](const Stage& st, int n0) {
+        double v[E];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int j = 0; j < MR; ++j) {
+                double acc = 0.0;
+#pragma unroll
+                for (int i = 0; i < L; ++i) {
+                    int c0, c1;
+                    piece_dot<FMT>(st.wv[r][i], act[j][i], c0, c1);
+                    acc += piece_term<FMT, PLAIN>(c0, c1, st.sc[r][i], shA[j][i], i * T + tl);
+                }
+                v[r * MR + j] = acc;
+            }
+        }
+        // reduce-scatter over the team: each step halves the values a lane carries (E - 1
+        // exchanges in all: permlane swaps across lane bits 5 and 4, DPP below), then plain
+        // steps finish the sums over the team's T lanes
+        int o = T >> 1;
+#pragma unroll
+        for (int h = E / 2; h >= 1; h >>= 1, o >>= 1) {
+#pragma unroll
+            for (int i = 0; i < h; ++i) v[i] = xchg_add(v[i], v[i + h], o, lane);
+        }
+        double tot = v[0];
+#pragma unroll
+        for (; o > 0; o >>= 1) tot = xsum(tot, o);
+        const int n = n0 + er * NT + team;
+        if (epilane && n < a.N && ej < a.M) {
+            if (a.acc_out) {
+                a.acc_out[(int64_t)ej * a.N + n] = (int64_t)tot;
+            } else {
+                // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw
+                // and the finished Sa * 2^-W need no operand flush
+                float y = fmul_f(fmul_f((float)tot, st.sw), sa2[ej]);
+                if (out) {
+                    float* op = out + (int64_t)ej * a.ors + n;
+                    if (a.flags & OTPU_ASCALE) y = fadd(fmul(*op, a.alpha[ej]), y);
+                    else if (a.flags & OTPU_ACC) y = fadd(*op, y);
+                    *op = y;
+                }
+                if (a.flags & OTPU_RMAX) atomicMax(a.rmax_key + ej, fkey_f(y));
+                if (a.best) {
+                    uint64_t cand = ((uint64_t)fkey_f(y) << 32) | (uint32_t)~(uint32_t)(a.base + n);
+                    best = cand > best ? cand : best;
+                }
+            }
+        }
+    };
+
+    // one stage per wave: the loads of an iteration go out together and the waves of the SIMD
+    // (5-8 resident) overlap each other's memory latency; a second register stage per wave
+    // costs occupancy and measured slower on MI355X
+    if constexpr (QIN) {
+        // the first rows stream in while the workgroup quantizes the activation row
+        Stage st;
+        const int nfirst = wave * RW;
+        if (nfirst < a.N) load(st, nfirst);
+        qin_prologue<FMT, L, T>(a, b, act[0], shA[0], sa2[0]);
+        for (int n0 = nfirst; n0 < a.N; n0 += stride) {
+            if (n0 != nfirst) load(st, n0);
+            compute(st, n0);
+        }
+    } else {
+        for (int n0 = wave * RW; n0 < a.N; n0 += stride) {
+            Stage st;
+            load(st, n0);
+            compute(st, n0);
+        }
+    }
+    if (a.best) {                               // one atomic per workgroup
+        __shared__ uint64_t red[4];
+        best = wave_max_u64(best);
+        if (lane == 0) red[threadIdx.x >> 6] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t m = red[0];
+            for (int i = 1; i < (int)(blockDim.x >> 6); ++i) m = red[i] > m ? red[i] : m;
+            if (m) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)m);
+        }
+    }
+}
+
+template <int FMT, int MR, int L, bool PLAIN>
+__global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
+    if (a.T == 64) gemv_body<FMT, MR, L, 64, PLAIN>(a);
+    else if (a.T == 32) gemv_body<FMT, MR, L, 32, PLAIN>(a);
+    else gemv_body<FMT, MR, L, 16, PLAIN>(a);
+}
+
+// MM with the QACT of its one activation row in the prologue
+template <int FMT, int L, bool PLAIN>
+__global__ __launch_bounds__(256) void gemv_qin_kernel(MMArgs a) {
+    if (a.T == 64) gemv_body<FMT, 1, L, 64, PLAIN, true>(a);
+    else if (a.T == 32) gemv_body<FMT, 1, L, 32, PLAIN, true>(a);
+    else gemv_body<FMT, 1, L, 16, PLAIN, true>(a);
+}
+
+// resident workgroups per CU the streaming grid aims for: 16 for one piece a lane (short rows,
+// more waves), else 8 (measured on MI355X); OTPU_GEMV_BLOCKS_PER_CU overrides
+inline int gemv_blocks_per_cu(int L) {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("OTPU_GEMV_BLOCKS_PER_CU");
+        int x = e ? atoi(e) : 0;
+        v = (x > 0 && x <= 64) ? x : 0;
+    }
+    return v ? v : (L == 1 ? 16 : 8);
+}
+
+template <int FMT, int MR, int L>
+void launch_one(const MMArgs& a, int batch, hipStream_t s) {
+    static_assert(fits<FMT, 1, L>(), "one activation row always fits");
+    if constexpr (fits<FMT, MR, L>()) {
+        constexpr int R = rows_per_team<L, MR>();
+        const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
+        // about 8 resident workgroups per CU over the whole batch; each wave then streams
+        // many row groups (its activation registers are loaded once)
+        int64_t blocks = (waves + 3) / 4;
+        int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L) / batch;
+        if (cap < 1) cap = 1;
+        if (blocks > cap) blocks = cap;
+        if (a.flags & (OTPU_UNIT | OTPU_RSC))
+            gemv_kernel<FMT, MR, L, true><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+        else
+            gemv_kernel<FMT, MR, L, false><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+    }
+}
+
+template <int FMT, int MR>
+void launch_L(const MMArgs& a, int L, int batch, hipStream_t s) {
+    switch (L) {
+        case 1: launch_one<FMT, MR, 1>(a, batch, s); break;
+        case 2: launch_one<FMT, MR, 2>(a, batch, s); break;
+        case 3: launch_one<FMT, MR, 3>(a, batch, s); break;
+        case 4: launch_one<FMT, MR, 4>(a, batch, s); break;
+        case 5: launch_one<FMT, MR, 5>(a, batch, s); break;
+        case 6: launch_one<FMT, MR, 6>(a, batch, s); break;
+        default: launch_one<FMT, MR, 8>(a, batch, s); break;
+    }
+}
+
+template <int FMT>
+void launch_fmt(const MMArgs& a, int mr, int L, int batch, hipStream_t s) {
+    if (mr == 1) launch_L<FMT, 1>(a, L, batch, s);
+    else if (mr == 2) launch_L<FMT, 2>(a, L, batch, s);
+    else launch_L<FMT, 4>(a, L, batch, s);
+}
+
+template <int FMT, int L>
+void launch_qin(const MMArgs& a, int batch, hipStream_t s) {
+    constexpr int R = rows_per_team<L, 1>();
+    const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
+    int64_t blocks = (waves + 3) / 4;
+    int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L) / batch;
+    if (cap < 1) cap = 1;
+    if (blocks > cap) blocks = cap;
+    if (a.flags & (OTPU_UNIT | OTPU_RSC))
+        gemv_qin_kernel<FMT, L, true><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+    else
+        gemv_qin_kernel<FMT, L, false><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+}
+
+template <int FMT>
+void launch_qin_fmt(const MMArgs& a, int L, int batch, hipStream_t s) {
+    switch (L) {
+        case 1: launch_qin<FMT, 1>(a, batch, s); break;
+        case 2: launch_qin<FMT, 2>(a, batch, s); break;
+        case 3: launch_qin<FMT, 3>(a, batch, s); break;
+        case 4: launch_qin<FMT, 4>(a, batch, s); break;
+        case 5: launch_qin<FMT, 5>(a, batch, s); break;
+        case 6: launch_qin<FMT, 6>(a, batch, s); break;
+        default: launch_qin<FMT, 8>(a, batch, s); break;
+    }
+}
+
+
+}  // namespace otpu

@@ -115,6 +115,61 @@ def test_mm_ranges_refusals(X):
                X.stream())
 
 
+@pytest.mark.parametrize("fmt,K,width,nsum,mul", [
+    ("int4", 1024, 1024, 1, False), ("int4", 1024, 1024, 12, False), ("int4", 2048, 2048, 1, False),
+    ("int4", 3072, 256, 1, True), ("fp4", 1536, 512, 2, True), ("int8", 1024, 1024, 3, False),
+    ("int8", 3072, 384, 1, True), ("int8", 2560, 2560, 1, False),
+])
+def test_mm_qin(X, fmt, K, width, nsum, mul):
+    """QACT + MM in one launch: each range's output equals QACT (oracle) of the range of the
+    folded (and multiplied) row followed by the oracle MM on that range's weight columns."""
+    import torch
+    rng = np.random.default_rng(K + width + nsum)
+    N = 300
+    rows, srows = _weights(rng, N, K, fmt)
+    xs = spread(rng, nsum, K)
+    xm = spread(rng, 1, K) if mul else None
+    src = xs[0:1]
+    for i in range(1, nsum):
+        src = F.add(src, xs[i:i + 1])
+    if mul:
+        src = F.mul(src, xm)
+    R = K // width
+    bpb = 128 if fmt == "int8" else 64
+    say("mm_qin", fmt, K, width, nsum, mul)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    xd, wd, sd = d(xs), d(rows), d(srows)
+    xmd = d(xm) if mul else None
+    out = torch.full((R, N), 7.0, dtype=torch.float32, device="cuda")
+    X.call("otpu_mm_qin", X.ptr(xd), X.ptr(xmd), nsum, K, K, width, X.ptr(wd), rows.shape[1], X.ptr(sd),
+           srows.shape[1], N, X.FMT[fmt], 0, 0, X.ptr(out), N, N, X.stream())
+    got = out.cpu().numpy()
+    for r in range(R):
+        q, Sa, da = F.quantize_mx(src[:, r * width:(r + 1) * width], 32)
+        part = rows[:, r * width // 128 * bpb:(r + 1) * width // 128 * bpb]
+        y = MM.mm(q, Sa, da, part, srows, fmt, width, k0=r * width // 128)
+        assert same_bits(got[r:r + 1], y), f"range {r}"
+
+
+def test_acc_rows(X):
+    import torch
+    rng = np.random.default_rng(9)
+    p = (rng.standard_normal((5, 1000)) * np.exp(rng.uniform(-30, 30, (5, 1000)))).astype(np.float32)
+    old = rng.standard_normal(1000).astype(np.float32)
+    pd, od = torch.from_numpy(p).cuda(), torch.from_numpy(old).cuda()
+    out = torch.empty(1000, dtype=torch.float32, device="cuda")
+    X.call("otpu_acc_rows", X.ptr(pd), 5, 1000, 1000, None, X.ptr(out), X.stream())
+    y = p[0]
+    for i in range(1, 5):
+        y = F.add(y, p[i])
+    assert same_bits(out.cpu().numpy(), y)
+    X.call("otpu_acc_rows", X.ptr(pd), 5, 1000, 1000, X.ptr(od), X.ptr(out), X.stream())
+    y = old
+    for i in range(5):
+        y = F.add(y, p[i])
+    assert same_bits(out.cpu().numpy(), y)
+
+
 def _host_layers(chain):
     return [{k: (r.cpu().numpy(), s.cpu().numpy()) for k, (r, s) in w.items()} for w in chain.layers]
 
@@ -141,8 +196,11 @@ def test_chain_layers_small(X):
         assert same_bits(ch.gu.cpu().numpy(), mid["gu"])
         assert same_bits(yd.cpu().numpy(), y0)
     x = rng.standard_normal((1, 256)).astype(np.float32)
-    y = ch.step(x).cpu().numpy()
-    assert same_bits(y, CH.step(x, host, "int4", 512, 768))
+    want = CH.step(x, host, "int4", 512, 768)
+    ch.fused = False
+    assert same_bits(ch.step(x).cpu().numpy(), want)
+    ch.fused = True
+    assert same_bits(ch.step(x).cpu().numpy(), want)
 
 
 def test_chain_c4_full_and_graph(X):
@@ -169,8 +227,19 @@ def test_chain_c4_full_and_graph(X):
     say("nonzero outputs per layer", nonzero)
     assert nonzero[0] > 900
     want = xo
-    say("chain c4: eager step")
+    say("chain c4: eager step, fused and unfused")
     assert same_bits(ch.step(x).cpu().numpy(), want)
+    ch.fused = False
+    assert same_bits(ch.step(x).cpu().numpy(), want)
+    ch.fused = True
+    say("chain c4: layers on N(0,1) inputs, fused")
+    for l in (0, 13, 27):                          # mid-stack layers on live (nonzero) inputs
+        xl = rng.standard_normal((1, 1024)).astype(np.float32)
+        ch.x.copy_(torch.from_numpy(xl).cuda())
+        ch.layer_fused(l, ch.x, 1, ch.parts[0])
+        yl = torch.empty((1, 1024), dtype=torch.float32, device="cuda")
+        X.call("otpu_acc_rows", X.ptr(ch.parts[0]), ch.R, 1024, 1024, None, X.ptr(yl), X.stream())
+        assert same_bits(yl.cpu().numpy(), CH.layer(xl, host[l], "int4")[0]), f"fused layer {l}"
     say("chain c4: graph")
     ch.capture()
     for i in range(3):
