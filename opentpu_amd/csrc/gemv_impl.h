@@ -1,19 +1,20 @@
-// MM for few activation rows (decode GEMV, M <= 4 per launch): the weight-streaming kernel,
-// the LM head with the greedy argmax fused into its epilogue, and VOP ARGMAX.
-// Semantics: opentpu/isasim.py:706-910 (MM), :1141-1152 (ARGMAX), docs/isa.md:226-305.
+// The decode GEMV kernel (MM for few activation rows, M <= 4 per launch), the LM head's variant
+// with the greedy argmax fused into its epilogue, and the variant that quantizes its activation
+// row in the prologue.  Semantics: opentpu/isasim.py:706-910 (MM), docs/isa.md:226-305.
 //
 // Layout of the work.  A weight row is cut into 16-byte pieces (int8: 16 elements, half a
-// 32-group; 4-bit: 32 elements, one 32-group).  A wave owns R weight rows at a time and lane l
-// takes pieces l, l+64, l+128, .. of each (L = ceil(pieces/64) per lane), so every load is a
-// 16-byte global_load_dwordx4 and a wave's load covers 1 KB of one row.  The activation pieces
-// a lane needs are the same for every row: they are loaded once, into registers (4-bit: split
-// into even / odd element bytes to meet the nibbles).  Per piece:
+// 32-group; 4-bit: 32 elements, one 32-group).  A team of T lanes (16, 32 or 64) owns a row, lane
+// tl taking pieces tl, tl + T, .. (L a lane), so every load is a 16-byte global_load_dwordx4;
+// a wave streams R rows per team per iteration (16 rows a wave for one activation row).  The
+// activation pieces a lane needs are the same for every row: they are loaded once, into
+// registers (4-bit: split into even / odd element bytes to meet the nibbles).  Per piece:
 //   int8   c = 4 x v_dot4_i32_i8
 //   int4   c = 8 x v_dot4 on (nibble << 4) bytes, then >> 4 (exact)
 //   fp4    E2M1 codes through two v_perm_b32 tables and a sign select, then 8 x v_dot4
-// then B = m << (W - dw - da) (0 where the shift is negative) and an int64 multiply-add.  The
-// wave reduces each row's int64 partials with shuffles and R*M lanes run the fp32 epilogue
-// (three FTZ products) and store.  Scale rows are read per lane piece (4 lanes share a word).
+// then the term (m c) 2^(W - dw - da) (0 where the shift is negative) as an exact double.  A
+// team reduce-scatters its rows' sums (v_permlane32/16_swap across lane bits 5 and 4, DPP
+// below), and the lanes that end with a row's sum run the fp32 epilogue (cvt of the exact sum,
+// then the FTZ products) and store.  Scale rows are read per lane piece (4 lanes share a word).
 #pragma once
 #include <cstdlib>
 
