@@ -38,9 +38,9 @@ struct MMArgs {
 constexpr int QIN_KMAX = 4096;     // columns a prologue QACT holds in LDS
 constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds
 
-// rows a team takes per iteration: with one piece a lane, 16 rows' loads in flight per wave for
-// one activation row (measured best on MI355X: 8 gave 3% less, 32 no more), fewer as activation
-// rows add sums to carry (R * MR stays 16)
+// rows a team takes per iteration: 16 rows' loads in flight per wave for one activation row
+// with one piece a lane (measured best on MI355X: 8 gave 3% less, 32 no more); 8 a team with four
+// or more pieces a lane (the LM head: 4% over 2); fewer as activation rows add sums to carry
 #ifndef OTPU_GEMV_R1
 #define OTPU_GEMV_R1 16
 #endif
@@ -51,10 +51,10 @@ constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds
 #define OTPU_GEMV_R2 2
 #endif
 #ifndef OTPU_GEMV_R4
-#define OTPU_GEMV_R4 2
+#define OTPU_GEMV_R4 8
 #endif
 constexpr int rows_per_team_rt(int L, int mr) {
-    return L >= 4 ? OTPU_GEMV_R4 : (L == 1 ? OTPU_GEMV_R1 / mr : OTPU_GEMV_R2);
+    return L >= 4 ? (OTPU_GEMV_R4 / mr > 0 ? OTPU_GEMV_R4 / mr : 1) : (L == 1 ? OTPU_GEMV_R1 / mr : OTPU_GEMV_R2);
 }
 template <int L, int MR>
 constexpr int rows_per_team() { return rows_per_team_rt(L, MR); }

@@ -465,8 +465,8 @@ __global__ __launch_bounds__(256) void gemv_qin_kernel(MMArgs a) {
     else gemv_body<FMT, 1, L, 16, PLAIN, true>(a);
 }
 
-// resident workgroups per CU the streaming grid aims for: 16 for one piece a lane (short rows,
-// more waves), else 8 (measured on MI355X); OTPU_GEMV_BLOCKS_PER_CU overrides
+// workgroups per CU the streaming grid aims for: 16 for one piece a lane and for four or more
+// (the LM head: 4% over 8), else 8 (measured on MI355X); OTPU_GEMV_BLOCKS_PER_CU overrides
 inline int gemv_blocks_per_cu(int L) {
     static int v = -1;
     if (v < 0) {
@@ -474,7 +474,7 @@ inline int gemv_blocks_per_cu(int L) {
         int x = e ? atoi(e) : 0;
         v = (x > 0 && x <= 64) ? x : 0;
     }
-    return v ? v : (L == 1 ? 16 : 8);
+    return v ? v : ((L == 1 || L >= 4) ? 16 : 8);
 }
 
 template <int FMT, int MR, int L>
