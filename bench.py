@@ -154,7 +154,9 @@ def lm_head(steps, warmup):
     return ms, int(tok.item())
 
 
-def gemm(steps, warmup):
+def gemm(steps, warmup, row_mode=True):
+    """The c3 prefill GEMM, RSC weights; activations ROW-quantized (the headline: one scale a
+    row, a single exact plane) or MX (group offsets: several planes)."""
     import torch
 
     from opentpu_amd import _lib as X
@@ -164,7 +166,7 @@ def gemm(steps, warmup):
     W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
     rows, srows = quant.quantize_mxu(W, "int8", rsc=True)
     x = torch.randn((M, K), generator=gen, device="cuda")
-    q, Sa, da = fp32.quantize_mx(x, 32, row_mode=True)
+    q, Sa, da = fp32.quantize_mx(x, 32, row_mode=row_mode)
     out = torch.empty((M, N), dtype=torch.float32, device="cuda")
 
     def step():
@@ -260,7 +262,9 @@ def summarize(outdir):
 
 
 def cpu_baseline(seconds=10.0):
-    """The C oracle (OpenMP) on this host: one c2 GEMV repeated for about `seconds`."""
+    """The C oracle (OpenMP) on this host: one c2 GEMV repeated for about `seconds` on
+    min(16, cores) threads; beside it (in `also`) the same C code on one thread and the numpy
+    oracle (float64 group sums, the reference simulator's method), each on a few calls."""
     from oracle import cpu as OC
     from oracle import formats as Q
     from oracle import fp32 as F
@@ -279,9 +283,23 @@ def cpu_baseline(seconds=10.0):
     for _ in range(reps):
         OC.mm(q, Sa, da, rows, srows, "int4", K)
     dt = (time.perf_counter() - t0) / reps
+    OC.threads(1)
+    t0 = time.perf_counter()
+    for _ in range(20):
+        OC.mm(q, Sa, da, rows, srows, "int4", K)
+    dt1 = (time.perf_counter() - t0) / 20
+    OC.threads(threads)
+    from oracle import mm as MM
+    t0 = time.perf_counter()
+    for _ in range(3):
+        MM.mm(q, Sa, da, rows, srows, "int4", K)
+    dtn = (time.perf_counter() - t0) / 3
     return {"value": round(c2_bytes() / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"c2 int4 GEMV 6144x2048, {reps} calls of the C oracle (oracle/cpu_mm.c, OpenMP), "
-                      f"{dt * 1e3:.2f} ms per call"}
+                      f"{dt * 1e3:.2f} ms per call",
+            "also": {"c_1_thread_GBps": round(c2_bytes() / dt1 / 1e9, 3), "c_1_thread_ms": round(dt1 * 1e3, 2),
+                     "numpy_oracle_GBps": round(c2_bytes() / dtn / 1e9, 3), "numpy_oracle_ms": round(dtn * 1e3, 1),
+                     "host_cores": os.cpu_count()}}
 
 
 def main():
@@ -349,6 +367,11 @@ def main():
         extra["c3_gemm_row_x_rsc"] = {"us": round(ms3 * 1e3, 2), "TOPS": round(tops, 2),
                                       "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         print(f"[c3] {extra['c3_gemm_row_x_rsc']}", file=sys.stderr, flush=True)
+        ms3m = gemm(5, 1, row_mode=False)
+        tops = 2 * 512 * 2048 * 8192 / (ms3m * 1e-3) / 1e12
+        extra["c3_gemm_mx_x_rsc"] = {"us": round(ms3m * 1e3, 2), "TOPS": round(tops, 2),
+                                     "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        print(f"[c3 mx] {extra['c3_gemm_mx_x_rsc']}", file=sys.stderr, flush=True)
 
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
