@@ -42,7 +42,11 @@ struct GemmArgs {
 };
 
 // byte offset of 16-byte chunk c of tile row r (rows of 128 bytes, chunks XOR-swizzled)
-__device__ __forceinline__ int swz(int r, int c) { return r * GBK + ((c ^ ((r >> 1) & 7)) << 4); }
+// The 16-byte slot of chunk c in row r is c ^ f(r), f(r) = ((r >> 1) & 7) ^ ((r & 1) << 2): the
+// 8 rows a ds_read_b128 fragment's lanes 0-7 (and 8-15) read land in 8 distinct slots of a 128-byte
+// bank window, and its 16 rows in 16 distinct (row parity, slot) pairs of a 256-byte one.
+__device__ __forceinline__ int rowswz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+__device__ __forceinline__ int swz(int r, int c) { return r * GBK + ((c ^ rowswz(r)) << 4); }
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
 
@@ -123,7 +127,7 @@ constexpr int RING = NS * STAGE > 2 * 2 * GBM * GBK ? NS * STAGE : 2 * 2 * GBM *
 static_assert(RBK == 64 || RBK == 128, "ring stages of 64 or 128 bytes");
 static_assert(NS >= 2 && (NS - 2) * LPS <= 63, "vmcnt holds at most 63");
 
-__device__ __forceinline__ int rswz(int r) { return RBK == 128 ? (r >> 1) & 7 : (r >> 2) & 3; }
+__device__ __forceinline__ int rswz(int r) { return RBK == 128 ? rowswz(r) : (r >> 2) & 3; }
 __device__ __forceinline__ int rof(int r, int c) { return r * RBK + ((c ^ rswz(r)) << 4); }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
