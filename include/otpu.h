@@ -157,6 +157,18 @@ int otpu_pack_int8(const float* W, int N, int K, int64_t ldw, int rsc, uint8_t* 
 int otpu_pack_x4(const float* W, int N, int K, int64_t ldw, int fmt, uint8_t* rows, int64_t rs,
                  uint8_t* srows, int64_t srs, otpu_stream_t stream);
 
+/* A weight image in the reference machine's grouped layout (docs/isa.md "Weight groups";
+ * opentpu/quant.py:634-808: group_rows / hash_rows / group_scales for a machine of wg lanes)
+ * back to the natural rows every MM entry point streams: the inverses of group_rows (with the
+ * channel hash of hash_rows when at >= 0: the image's byte address on that machine, a multiple
+ * of wg * 128) and of group_scales.  data: ceil(N / R) groups of grp_row_bytes (R = wg int8,
+ * 2 wg 4-bit; wg = 1 the natural rows); rows: N rows of rs >= row_bytes(K); areas: the groups'
+ * scale areas; srows: N scale rows of srs >= scale_bytes(K).  MM KT's pairs are not taken. */
+int otpu_ungroup_rows(const uint8_t* data, int N, int K, int wg, int fmt, int64_t at, uint8_t* rows,
+                      int64_t rs, otpu_stream_t stream);
+int otpu_ungroup_scales(const uint8_t* areas, int N, int K, int wg, int fmt, int rsc, uint8_t* srows,
+                        int64_t srs, otpu_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,6 +36,8 @@ SIGNATURES = {
     "otpu_vmul": ([_P, _P, _P, _L, _P], _I),
     "otpu_mm_qin": ([_P, _P, _I, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _L, _P], _I),
     "otpu_acc_rows": ([_P, _I, _L, _I, _P, _P, _P], _I),
+    "otpu_ungroup_rows": ([_P, _I, _I, _I, _I, _L, _P, _L, _P], _I),
+    "otpu_ungroup_scales": ([_P, _I, _I, _I, _I, _I, _P, _L, _P], _I),
 }
 
 

@@ -57,3 +57,78 @@ def quantize_mxu(W, fmt: str, rsc: bool = False):
         X.call("otpu_pack_x4", X.ptr(Wd), N, K, K, X.FMT[fmt], X.ptr(rows), rb, X.ptr(srows), srs,
                X.stream())
     return (X.host(rows), X.host(srows)) if numpy_in else (rows, srows)
+
+
+# ------------------------------------------------------------------------------ weight groups
+# A reference machine of WG lanes stores an [N, K] weight in groups of R rows (R = WG int8, 2 WG
+# 4-bit, 1 at WG = 1), optionally with its chunks' lanes in the channel hash's order at the
+# image's address (`docs/isa.md` "Weight groups"; `opentpu/quant.py:634-808`, `grouped`). The
+# converters below turn such an image back into the natural rows every MM entry point streams,
+# on the GPU (`otpu_ungroup_rows`, `otpu_ungroup_scales`). MM KT's pairs are not taken.
+
+def grp_r(fmt: str, wg: int) -> int:
+    """Rows of a group on a machine of wg lanes."""
+    return wg if wg == 1 or fmt == "int8" else 2 * wg
+
+
+def grp_row_bytes(K: int, fmt: str, wg: int) -> int:
+    """The group stride of a grouped [., K] matrix (`opentpu/quant.py:672-679`)."""
+    if wg == 1 or fmt == "int8":
+        return row_bytes(K, fmt) * wg
+    if K % D:
+        raise ValueError(f"inner dimension {K} is not a multiple of D={D}")
+    return (K // D) * wg * D
+
+
+def grp_scale_bytes(K: int, fmt: str, wg: int, rsc: bool = False) -> int:
+    """The group scale stride (`opentpu/quant.py:682-690`)."""
+    if K % D:
+        raise ValueError(f"inner dimension {K} is not a multiple of D={D}")
+    R = grp_r(fmt, wg)
+    sb = {"int8": 1, "int4": 4, "fp4": 4, "nvfp4": 8}[fmt]
+    p = 4 * R if rsc or fmt == "int8" else ((16 if R == 1 else 8 * R) if fmt == "nvfp4"
+                                            else (8 if R == 1 else 4 * R))
+    n = p if rsc else p + (K // D) * R * sb
+    return -(-n // p) * p
+
+
+def _check_image(a, G: int, width: int, what: str):
+    if a.dim() != 2 or a.shape[0] < G or a.shape[1] != width or not a.is_contiguous():
+        raise ValueError(f"{what}: expected a contiguous [{G}, {width}] uint8 image, got {tuple(a.shape)}")
+
+
+def ungroup_rows(data, N: int, K: int, wg: int, fmt: str, at: int | None = None):
+    """A grouped element image [ceil(N / R), grp_row_bytes] (uint8; `at`: its byte address on a
+    machine with the channel hash, None: unhashed) -> natural rows [N, row_bytes] on the GPU.
+    numpy in, numpy out."""
+    if fmt not in MXU_FORMATS:
+        raise ValueError(f"unknown MXU format {fmt!r}")
+    numpy_in = X.is_numpy(data)
+    d = X.dev(data, np.uint8)
+    G = -(-N // grp_r(fmt, wg))
+    _check_image(d, G, grp_row_bytes(K, fmt, wg), "ungroup_rows")
+    rows = X.empty((N, row_bytes(K, fmt)), np.uint8)
+    X.call("otpu_ungroup_rows", X.ptr(d), N, K, wg, X.FMT[fmt], -1 if at is None else int(at), X.ptr(rows),
+           rows.shape[1], X.stream())
+    return X.host(rows) if numpy_in else rows
+
+
+def ungroup_scales(areas, N: int, K: int, wg: int, fmt: str, rsc: bool = False):
+    """Grouped scale areas [ceil(N / R), grp_scale_bytes] -> natural scale rows [N, scale_bytes]
+    on the GPU (reserved words and padding 0). numpy in, numpy out."""
+    if fmt not in MXU_FORMATS:
+        raise ValueError(f"unknown MXU format {fmt!r}")
+    numpy_in = X.is_numpy(areas)
+    a = X.dev(areas, np.uint8)
+    G = -(-N // grp_r(fmt, wg))
+    _check_image(a, G, grp_scale_bytes(K, fmt, wg, rsc), "ungroup_scales")
+    srows = X.empty((N, scale_bytes(K, fmt, rsc)), np.uint8)
+    X.call("otpu_ungroup_scales", X.ptr(a), N, K, wg, X.FMT[fmt], int(bool(rsc)), X.ptr(srows), srows.shape[1],
+           X.stream())
+    return X.host(srows) if numpy_in else srows
+
+
+def ungrouped(data, areas, N: int, K: int, wg: int, fmt: str, at: int | None = None, rsc: bool = False):
+    """The inverse of the reference's `quant.grouped(q, s, fmt, K, wg, at=at)` without KT
+    (`opentpu/quant.py:811-826`): an image's (data, scale areas) -> (rows, scale rows) for MM."""
+    return ungroup_rows(data, N, K, wg, fmt, at), ungroup_scales(areas, N, K, wg, fmt, rsc)

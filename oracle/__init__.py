@@ -13,6 +13,8 @@ Modules
            (int8x, RSC, int4x / fp4x6 m-search, nvfp4 decode), dequantization.
   mm       MM: exact per-group int32 sums, int64 shift-accumulate, the fp32 epilogue,
            ACC / ASCALE / RMAX; ARGMAX and greedy selection.
+  groups   the reference machine's grouped / channel-hashed weight images (WG lanes) and their
+           inverses, built byte address by byte address from the layout's formulas.
   cpu      ctypes binding of `cpu_mm.c` (the same functions in C with OpenMP), the fast
            checker at full sizes and the CPU baseline timer.
 
