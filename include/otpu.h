@@ -150,8 +150,9 @@ int otpu_argmax(const float* x, int rows, int cols, int64_t ldx, int64_t base, f
  * reference: it packs on the host in numpy).
  *   otpu_pack_int8: int8x (quant.py:316-322, rsc = 0; scale rows of 4 + 4*ceil(KB/4) bytes) or
  *   RSC rows (runtime.py:66-76 with row=True, rsc = 1; scale rows of 4 bytes).
- *   otpu_pack_x4: int4x / fp4x6 (quant.py:325-367; fmt OTPU_INT4 or OTPU_FP4): element rows of
- *   ceil(K/256)*128 bytes, scale rows of 8 + 8*ceil(KB/2) bytes. */
+ *   otpu_pack_x4: int4x / fp4x6 (quant.py:325-367; fmt OTPU_INT4 or OTPU_FP4) or nvfp4 with a
+ *   per-row scale (quant.py:368-400; fmt OTPU_NVFP4): element rows of ceil(K/256)*128 bytes,
+ *   scale rows of 8 + 8*ceil(KB/2) bytes (nvfp4: 16 + 16*ceil(KB/2)). */
 int otpu_pack_int8(const float* W, int N, int K, int64_t ldw, int rsc, uint8_t* rows,
                    int64_t rs, uint8_t* srows, int64_t srs, otpu_stream_t stream);
 int otpu_pack_x4(const float* W, int N, int K, int64_t ldw, int fmt, uint8_t* rows, int64_t rs,
@@ -168,6 +169,24 @@ int otpu_ungroup_rows(const uint8_t* data, int N, int K, int wg, int fmt, int64_
                       int64_t rs, otpu_stream_t stream);
 int otpu_ungroup_scales(const uint8_t* areas, int N, int K, int wg, int fmt, int rsc, uint8_t* srows,
                         int64_t srs, otpu_stream_t stream);
+
+/* Checkpoint imports, exact (opentpu/quant.py:1070-1182, import_mxfp4 / import_nvfp4; the
+ * reference converts on the host in numpy).  codes: one E2M1 code (0..15, sign bit 3) a byte,
+ * [N, K] at ldc; rows / srows as otpu_pack_x4 writes them for fp4 / nvfp4.  status[n]: the
+ * reasons row n does not come in exactly in the asked format (0: it does):
+ *   otpu_import_mxfp4: e8m0 [N, K/32] at lde; fmt OTPU_FP4 or OTPU_NVFP4; status bits 1 an E8M0
+ *   NaN, 2 a K-block spanning more than 5 octaves (no fp4), 4 an fp4 dw above 255, 8 fp4's Sw
+ *   outside fp32's normal range, 16 a row spanning more than 17 octaves (no nvfp4; set by the
+ *   nvfp4 call), 32 nvfp4's Sw outside the normal range (nvfp4 call).
+ *   otpu_import_nvfp4: scales [N, K/16] E4M3 bytes at lds, ts the tensor scale; status bits 1 a
+ *   negative scale, 2 an E4M3 NaN, 4 a scale too far below the row's largest, 8 Sw outside
+ *   fp32's normal range. */
+int otpu_import_mxfp4(const uint8_t* codes, int64_t ldc, const uint8_t* e8m0, int64_t lde, int N, int K,
+                      int fmt, uint8_t* rows, int64_t rs, uint8_t* srows, int64_t srs, int32_t* status,
+                      otpu_stream_t stream);
+int otpu_import_nvfp4(const uint8_t* codes, int64_t ldc, const uint8_t* scales, int64_t lds, float ts,
+                      int N, int K, uint8_t* rows, int64_t rs, uint8_t* srows, int64_t srs,
+                      int32_t* status, otpu_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -17,8 +17,8 @@ INT8, INT4, FP4, NVFP4 = 0, 1, 2, 3
 FMT = {"int8": INT8, "int4": INT4, "fp4": FP4, "nvfp4": NVFP4}
 UNIT, ACC, RMAX, ASCALE, PAIR, RSC = 0x1, 0x2, 0x4, 0x8, 0x40, 0x80
 
-# every exported symbol and its argument types (P pointer, L int64, I int32)
-_P, _L, _I = C.c_void_p, C.c_int64, C.c_int
+# every exported symbol and its argument types (P pointer, L int64, I int32, F float)
+_P, _L, _I, _F = C.c_void_p, C.c_int64, C.c_int, C.c_float
 SIGNATURES = {
     "otpu_last_error": ([], C.c_char_p),
     "otpu_version": ([], _I),
@@ -38,6 +38,8 @@ SIGNATURES = {
     "otpu_acc_rows": ([_P, _I, _L, _I, _P, _P, _P], _I),
     "otpu_ungroup_rows": ([_P, _I, _I, _I, _I, _L, _P, _L, _P], _I),
     "otpu_ungroup_scales": ([_P, _I, _I, _I, _I, _I, _P, _L, _P], _I),
+    "otpu_import_mxfp4": ([_P, _L, _P, _L, _I, _I, _I, _P, _L, _P, _L, _P, _P], _I),
+    "otpu_import_nvfp4": ([_P, _L, _P, _L, _F, _I, _I, _P, _L, _P, _L, _P, _P], _I),
 }
 
 

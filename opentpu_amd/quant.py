@@ -1,6 +1,6 @@
 """The MXU's streamed weight formats: byte layouts (`opentpu/quant.py:287-308`) and the packers
 `quantize_mxu` (`opentpu/quant.py:510-523`) run on the GPU (HIP kernels, bit-exact with the
-reference's numpy: int8x, RSC rows, int4x, fp4x6)."""
+reference's numpy: int8x, RSC rows, int4x, fp4x6, nvfp4)."""
 from __future__ import annotations
 
 import numpy as np
@@ -37,10 +37,10 @@ def scale_bytes(K: int, fmt: str, rsc: bool = False) -> int:
 def quantize_mxu(W, fmt: str, rsc: bool = False):
     """W [N, K] fp32 -> (element rows uint8 [N, row_bytes], scale rows uint8 [N, scale_bytes]),
     packed on the GPU.  fmt "int8" (int8x; with rsc=True the RSC rows of one fp32 scale each,
-    `opentpu/runtime.py:66-76`), "int4" or "fp4".  numpy in, numpy out; tensors stay on the
-    device."""
-    if fmt not in ("int8", "int4", "fp4"):
-        raise ValueError(f"quantize_mxu: no GPU packer for {fmt!r}")
+    `opentpu/runtime.py:66-76`), "int4", "fp4" or "nvfp4" (`opentpu/quant.py:368-400`).  numpy
+    in, numpy out; tensors stay on the device."""
+    if fmt not in MXU_FORMATS:
+        raise ValueError(f"quantize_mxu: unknown MXU format {fmt!r}")
     numpy_in = X.is_numpy(W)
     Wd = X.dev(W, np.float32)
     N, K = Wd.shape
@@ -132,3 +132,86 @@ def ungrouped(data, areas, N: int, K: int, wg: int, fmt: str, at: int | None = N
     """The inverse of the reference's `quant.grouped(q, s, fmt, K, wg, at=at)` without KT
     (`opentpu/quant.py:811-826`): an image's (data, scale areas) -> (rows, scale rows) for MM."""
     return ungroup_rows(data, N, K, wg, fmt, at), ungroup_scales(areas, N, K, wg, fmt, rsc)
+
+
+# -------------------------------------------------------------------------- checkpoint imports
+class NotExact(ValueError):
+    """A checkpoint's quantized weights that no MXU format holds exactly (`opentpu/quant.py:1071`)."""
+
+
+def _status(st) -> int:
+    return int(np.bitwise_or.reduce(X.host(st).astype(np.int64))) if st.numel() else 0
+
+
+def import_mxfp4(codes, e8m0, want: str | None = None):
+    """An OCP MXFP4 matrix (E2M1 codes [N, K] one a byte, E8M0 exponents [N, K / 32]) in an MXU
+    format, exactly, converted on the GPU: (rows, scale rows, "fp4" | "nvfp4")
+    (`opentpu/quant.py:1084-1140`). fp4 where every K-block's live exponents span at most 5, else
+    nvfp4 where every row's span at most 17, else NotExact; want forces a format. numpy in,
+    numpy out."""
+    if want not in (None, "fp4", "nvfp4"):
+        raise ValueError(f"MXFP4 into {want!r}: fp4 or nvfp4")
+    numpy_in = X.is_numpy(codes)
+    c = X.dev(codes, np.uint8)
+    e = X.dev(e8m0, np.uint8)
+    N, K = c.shape
+    if K % D or tuple(e.shape) != (N, K // 32):
+        raise ValueError(f"MXFP4 [{N}, {K}] with scales {tuple(e.shape)}: blocks of 32, D = 128")
+    st = X.empty((N,), np.int32)
+    rows = X.empty((N, row_bytes(K, "fp4")), np.uint8)
+
+    def run(fmt):
+        srows = X.empty((N, scale_bytes(K, fmt)), np.uint8)
+        X.call("otpu_import_mxfp4", X.ptr(c), K, X.ptr(e), K // 32, N, K, X.FMT[fmt], X.ptr(rows), rows.shape[1],
+               X.ptr(srows), srows.shape[1], X.ptr(st), X.stream())
+        return srows, _status(st)
+
+    srows, s = run("nvfp4" if want == "nvfp4" else "fp4")
+    if s & 1:
+        raise NotExact("MXFP4: an E8M0 NaN scale")
+    fmt = "nvfp4"
+    if want != "nvfp4" and not s & 2:
+        if s & 4:
+            raise NotExact("MXFP4: a block more than 255 octaves below its row's top")
+        if s & 8:
+            raise NotExact("MXFP4: a row scale outside fp32's normal range")
+        fmt = "fp4"
+    elif want == "fp4":
+        raise NotExact("MXFP4: a K-block's exponents span more than fp4's 5 octaves")
+    else:
+        if want != "nvfp4":
+            srows, s = run("nvfp4")
+        if s & 16:
+            raise NotExact("MXFP4: a row's scales span more than 17 octaves, nvfp4's E4M3 holds 17 "
+                           "with mantissa 0")
+        if s & 32:
+            raise NotExact("MXFP4: a row scale outside fp32's normal range")
+    return (X.host(rows), X.host(srows), fmt) if numpy_in else (rows, srows, fmt)
+
+
+def import_nvfp4(codes, e4m3_scales, tensor_scale: float):
+    """An NVFP4 matrix (E2M1 codes [N, K] one a byte, E4M3 scales [N, K / 16], the per-tensor
+    fp32 scale) in the MXU's nvfp4, exactly, converted on the GPU: (rows, scale rows)
+    (`opentpu/quant.py:1143-1182`). numpy in, numpy out."""
+    numpy_in = X.is_numpy(codes)
+    c = X.dev(codes, np.uint8)
+    sc = X.dev(e4m3_scales, np.uint8)
+    N, K = c.shape
+    if K % D or tuple(sc.shape) != (N, K // 16):
+        raise ValueError(f"NVFP4 [{N}, {K}] with scales {tuple(sc.shape)}: groups of 16, D = 128")
+    st = X.empty((N,), np.int32)
+    rows = X.empty((N, row_bytes(K, "nvfp4")), np.uint8)
+    srows = X.empty((N, scale_bytes(K, "nvfp4")), np.uint8)
+    X.call("otpu_import_nvfp4", X.ptr(c), K, X.ptr(sc), K // 16, float(np.float32(tensor_scale)), N, K,
+           X.ptr(rows), rows.shape[1], X.ptr(srows), srows.shape[1], X.ptr(st), X.stream())
+    s = _status(st)
+    if s & 1:
+        raise NotExact("NVFP4: a negative E4M3 scale")
+    if s & 2:
+        raise NotExact("NVFP4: an E4M3 NaN scale")
+    if s & 4:
+        raise NotExact("NVFP4: a scale more than 14 octaves below its row's largest whose low bits an "
+                       "MXU subnormal does not hold")
+    if s & 8:
+        raise NotExact("NVFP4: a row scale outside fp32's normal range")
+    return (X.host(rows), X.host(srows)) if numpy_in else (rows, srows)

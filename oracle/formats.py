@@ -186,11 +186,75 @@ def pack_x4(W, fmt: str):
                              m=m.astype(np.uint8))
 
 
+E4M3_MAX, E2M1_MAX = 448.0, 6.0
+
+
+def e4m3_value(code):
+    """The non-negative E4M3 value of codes 0..126 (OCP: bias 7, subnormals at E = 0)."""
+    c = np.asarray(code, np.int64)
+    E, m = c >> 3, c & 7
+    return np.where(E == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * np.exp2(E - 7.0))
+
+
+def e4m3_code(a):
+    """Round non-negative float64 values to E4M3, to nearest with ties to the even mantissa,
+    saturating at 448 (code 126): the reference's grid rounding (`opentpu/quant.py:56-71`),
+    derived here from the binade (a / 2^e's three fraction bits) instead of a grid search."""
+    a = np.asarray(a, np.float64)
+    _, ex = np.frexp(np.where(a > 0, a, 1.0))             # exact exponent: a in [2^(ex-1), 2^ex)
+    e = (ex - 1).astype(np.int64)
+    sub = e < -6
+    q_sub = np.rint(np.minimum(a, 1.0) / 2.0 ** -9)        # multiples of the subnormal step
+    f = np.ldexp(a, -np.maximum(e, -6).astype(np.int32))   # [1, 2) for normals
+    q = np.rint((f - 1.0) * 8.0)                           # exact: f - 1 has <= 52 bits
+    code_n = ((e + 7) << 3) + q.astype(np.int64)           # q == 8 carries into the exponent
+    code = np.where(sub, q_sub.astype(np.int64), code_n)
+    code = np.where(a > 0, code, 0)
+    return np.minimum(code, 126)
+
+
+def pack_nv(W):
+    """nvfp4 rows with a per-row fp32 scale (`opentpu/quant.py:368-400`, `_nv`): ts = f32(row
+    amax / (448 * 6)) (1 for a zero row); per group of 16 the E4M3 scale s among
+    e4m3(group amax / ts * f / 6), f in SEARCH, with the least float64 squared error over the
+    group (numpy's sum; the first candidate wins ties; s = 1 where the group or s is 0); E2M1
+    codes of x / s; Sw = f32(16 ts)."""
+    W = np.asarray(W, np.float32)
+    N, K = W.shape
+    a = W.astype(np.float64)
+    ts = np.abs(a).max(-1, keepdims=True) / (E4M3_MAX * E2M1_MAX)
+    ts = np.where(ts == 0, 1.0, ts).astype(np.float32).astype(np.float64)
+    xb = a.reshape(N, K // 16, 16) / ts[..., None]
+    amax = np.abs(xb).max(-1)
+    best = None
+    for f in SEARCH:
+        s = e4m3_value(e4m3_code(amax * f / E2M1_MAX))
+        s = np.where((amax == 0) | (s == 0), 1.0, s)
+        q = np.sign(xb) * E2M1_MAG[_e2m1_code(xb / s[..., None])] * s[..., None]
+        err = ((q - xb) ** 2).sum(-1)
+        if best is None:
+            best = [s, q, err]
+        else:
+            k = err < best[2]
+            best = [np.where(k, s, best[0]), np.where(k[..., None], q, best[1]),
+                    np.where(k, err, best[2])]
+    s, q, _ = best
+    x = q / s[..., None]
+    mag = _e2m1_code(x)
+    code = (mag | np.where(np.signbit(x) & (mag != 0), 8, 0)).reshape(N, K)
+    rows = np.zeros((N, row_bytes(K, "nvfp4")), np.uint8)
+    rows[:, :K // 2] = pack_nibbles(code)
+    e4 = e4m3_code(s).reshape(N, K // D, NVG)
+    return rows, pack_scales("nvfp4", (16 * ts[:, 0]).astype(np.float32), e4=e4.astype(np.uint8))
+
+
 def quantize_mxu(W, fmt: str):
     if fmt == "int8":
         return pack_int8x(W)
     if fmt in ("int4", "fp4"):
         return pack_x4(W, fmt)
+    if fmt == "nvfp4":
+        return pack_nv(W)
     raise ValueError(f"no packer for {fmt!r} in the oracle")
 
 

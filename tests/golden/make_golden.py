@@ -1,12 +1,15 @@
-"""Write the golden vectors of the one function on this path that no closed form, known answer
-or scalar model pins: the reference's int4x / fp4x6 weight packer (`opentpu/quant.py:325-367`,
-`quantize_mxu(W, "int4" | "fp4")`), whose float64 multiplier search keeps the first of equal
-squared errors.
+"""Write the golden vectors of the functions on this path that no closed form, known answer
+or scalar model pins: the reference's 4-bit weight packers, whose float64 scale searches keep
+the first of equal squared errors in numpy's summation order:
+  * int4x / fp4x6 (`opentpu/quant.py:325-367`, `quantize_mxu(W, "int4" | "fp4")`) ->
+    `x4_packer.npz`;
+  * nvfp4 with a per-row scale (`opentpu/quant.py:368-400`, `quantize_mxu(W, "nvfp4")`) ->
+    `nv_packer.npz`.
 
 Run once, in the build container (the reference is at /root/reference and never travels):
     python tests/golden/make_golden.py
-It imports `opentpu.quant` from the reference and writes `x4_packer.npz` beside this file:
-the inputs (seeded fp32 weights) and the packed element and scale rows for each format.
+It imports `opentpu.quant` from the reference and writes the files beside this one: the inputs
+(seeded fp32 weights) and the packed element and scale rows for each format.
 """
 import os
 import sys
@@ -36,16 +39,17 @@ def inputs():
 def main():
     sys.path.insert(0, REF)
     from opentpu import quant as RQ                    # noqa: E402  (the reference)
-    out = {}
-    for name, W in inputs().items():
-        out[f"{name}_W"] = W
-        for fmt in ("int4", "fp4"):
-            rows, srows = RQ.quantize_mxu(W, fmt)
-            out[f"{name}_{fmt}_rows"] = rows
-            out[f"{name}_{fmt}_srows"] = srows
-    path = os.path.join(HERE, "x4_packer.npz")
-    np.savez_compressed(path, **out)
-    print(path, os.path.getsize(path), "bytes")
+    for fname, fmts in (("x4_packer.npz", ("int4", "fp4")), ("nv_packer.npz", ("nvfp4",))):
+        out = {}
+        for name, W in inputs().items():
+            out[f"{name}_W"] = W
+            for fmt in fmts:
+                rows, srows = RQ.quantize_mxu(W, fmt)
+                out[f"{name}_{fmt}_rows"] = rows
+                out[f"{name}_{fmt}_srows"] = srows
+        path = os.path.join(HERE, fname)
+        np.savez_compressed(path, **out)
+        print(path, os.path.getsize(path), "bytes")
 
 
 if __name__ == "__main__":

@@ -126,3 +126,40 @@ def test_layout_zero_block_and_error(fmt, bound):
     if fmt != "int8":
         _, _, m = Q.unpack_scales(sr, fmt, 5)
         assert m.min() >= 1 and m.max() <= 63
+
+
+def test_e4m3_rounding_is_nearest_even_on_the_grid():
+    """oracle e4m3_code (from the binade) against a bracket search of the E4M3 grid: nearest,
+    ties to the even code, saturating at 448; every grid value, every midpoint, and random
+    values over the whole range and past it."""
+    grid = Q.e4m3_value(np.arange(127))
+    for c in range(127):
+        assert grid[c] == _e4m3(c)
+    rng = np.random.default_rng(0)
+    a = np.concatenate([grid, (grid[1:] + grid[:-1]) / 2, rng.uniform(0, 500, 20000),
+                        np.exp2(rng.uniform(-16, 10, 20000)), [464.0, 480.0, 1e30, 2.0 ** -10]])
+    i = np.clip(np.searchsorted(grid, a), 1, 126)
+    lo, hi = grid[i - 1], grid[i]
+    want = np.where(a - lo < hi - a, i - 1, np.where(hi - a < a - lo, i, i - 1 + (i - 1) % 2))
+    want = np.where(a >= 448.0, 126, want)
+    assert np.array_equal(Q.e4m3_code(a), want)
+    assert Q.e4m3_code(np.array([2.0 ** -10]))[0] == 0          # tie with 0: the even code
+    assert Q.e4m3_code(np.array([464.0]))[0] == 126
+
+
+def test_nv_packer_layout_and_error():
+    """nvfp4 rows: Sw = 16 ts (ts = f32(amax / 2688)); the dequantized row is within half an E2M1
+    step of a scaled group of W; an all-zero row packs to Sw 16 and scale 1.0 (0x38)."""
+    rng = np.random.default_rng(1)
+    W = (rng.standard_normal((6, 384)) * 0.02).astype(np.float32)
+    W[4] = 0
+    rows, srows = Q.pack_nv(W)
+    assert rows.shape == (6, Q.row_bytes(384, "nvfp4")) and srows.shape == (6, 48)
+    Sw = srows[:, :4].copy().view(np.float32)[:, 0]
+    ts = (np.abs(W.astype(np.float64)).max(1) / 2688.0).astype(np.float32)
+    assert np.array_equal(Sw[[0, 1, 2, 3, 5]], (16 * ts[[0, 1, 2, 3, 5]].astype(np.float64)).astype(np.float32))
+    assert Sw[4] == 16.0 and np.all(srows[4, 16:40] == 0x38)
+    assert not np.any(srows[:, 40:]) and not np.any(srows[:, 4:16])
+    deq = Q.dequantize(rows, srows, "nvfp4", 384)
+    err = np.abs(deq - W.astype(np.float64))
+    assert err.max() <= np.abs(W).max() / 6 + 1e-12             # within an E2M1 step of amax
