@@ -188,6 +188,19 @@ int otpu_import_nvfp4(const uint8_t* codes, int64_t ldc, const uint8_t* scales, 
                       int N, int K, uint8_t* rows, int64_t rs, uint8_t* srows, int64_t srs,
                       int32_t* status, otpu_stream_t stream);
 
+/* The sampled decode's pick after the LM head (opentpu/llm/generate.py:323-337 Sampler and
+ * :492-557 reference_pick at one slice; the reference's device sampler, in its fp32 arithmetic):
+ * logits [V] (the LM head's, e.g. otpu_lm_head_argmax's logits output); pa / pb [V] the
+ * repetition penalty's factors (1/R and R at the context's ids, 1 elsewhere; both NULL: none);
+ * softcap c (0: none); top_k k in 1..64; itemp = f32(log2(e) / temperature); top_p; u [nu]
+ * uniforms, one pick each, to ids [nu].  status[0] = 1 when top_p keeps no token (the
+ * reference raises), else 0.  work: otpu_sample_work_bytes(V) bytes (also holds the km
+ * candidate values and ids after the call, km = k rounded up to 8).  Two kernels. */
+int64_t otpu_sample_work_bytes(int V);
+int otpu_sample(const float* logits, int V, const float* pa, const float* pb, double softcap, int k,
+                float itemp, float top_p, const float* u, int nu, void* work, int32_t* ids,
+                int32_t* status, otpu_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

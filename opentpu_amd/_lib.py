@@ -17,8 +17,8 @@ INT8, INT4, FP4, NVFP4 = 0, 1, 2, 3
 FMT = {"int8": INT8, "int4": INT4, "fp4": FP4, "nvfp4": NVFP4}
 UNIT, ACC, RMAX, ASCALE, PAIR, RSC = 0x1, 0x2, 0x4, 0x8, 0x40, 0x80
 
-# every exported symbol and its argument types (P pointer, L int64, I int32, F float)
-_P, _L, _I, _F = C.c_void_p, C.c_int64, C.c_int, C.c_float
+# every exported symbol and its argument types (P pointer, L int64, I int32, F float, D double)
+_P, _L, _I, _F, _D = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double
 SIGNATURES = {
     "otpu_last_error": ([], C.c_char_p),
     "otpu_version": ([], _I),
@@ -40,6 +40,8 @@ SIGNATURES = {
     "otpu_ungroup_scales": ([_P, _I, _I, _I, _I, _I, _P, _L, _P], _I),
     "otpu_import_mxfp4": ([_P, _L, _P, _L, _I, _I, _I, _P, _L, _P, _L, _P, _P], _I),
     "otpu_import_nvfp4": ([_P, _L, _P, _L, _F, _I, _I, _P, _L, _P, _L, _P, _P], _I),
+    "otpu_sample_work_bytes": ([_I], _L),
+    "otpu_sample": ([_P, _I, _P, _P, _D, _I, _F, _F, _P, _I, _P, _P, _P, _P], _I),
 }
 
 
