@@ -78,10 +78,8 @@ class Sampler:
     def candidates(self):
         """(values [kmax] fp32, ids [kmax] int32) of the last pick: the k largest logits."""
         km = self.samp.kmax
-        nb = -(-self.V // 64)
-        w = X.host(self.work).view(np.float32)
-        off = nb * 64 + nb
-        return w[off:off + km].copy(), w[off + 64:off + 64 + km].view(np.int32).copy()
+        w = X.host(self.work[:512]).view(np.float32)             # vs [64], then si [64]
+        return w[:km].copy(), w[64:64 + km].view(np.int32).copy()
 
 
 def pick(logits, samp: Sampling, context=(), u=0.5, softcap: float | None = None):
