@@ -324,7 +324,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=80)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c4,c5,copy (default: c1,c2s,c3,c4,c5); "
+    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c3r,c4,c5,copy (default: c1,c2s,c3,c4,c5; "
+                    "c3r: the ROW GEMM alone); "
                     "the headline c2 always runs, c2s adds its single-launch figure")
     ap.add_argument("--summarize", metavar="DIR", help="print a text summary of rocprofv3 CSV output and exit")
     args = ap.parse_args()
@@ -378,12 +379,13 @@ def main():
     if "c4" in only:
         extra["c4_decode_step"] = c4_step(10, 2)
         print(f"[c4] {extra['c4_decode_step']}", file=sys.stderr, flush=True)
-    if "c3" in only:
+    if "c3" in only or "c3r" in only:
         ms3 = gemm(5, 1)
         tops = 2 * 512 * 2048 * 8192 / (ms3 * 1e-3) / 1e12
         extra["c3_gemm_row_x_rsc"] = {"us": round(ms3 * 1e3, 2), "TOPS": round(tops, 2),
                                       "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         print(f"[c3] {extra['c3_gemm_row_x_rsc']}", file=sys.stderr, flush=True)
+    if "c3" in only:
         ms3m = gemm(5, 1, row_mode=False)
         tops = 2 * 512 * 2048 * 8192 / (ms3m * 1e-3) / 1e12
         extra["c3_gemm_mx_x_rsc"] = {"us": round(ms3m * 1e3, 2), "TOPS": round(tops, 2),
