@@ -201,6 +201,24 @@ int otpu_sample(const float* logits, int V, const float* pa, const float* pb, do
                 float itemp, float top_p, const float* u, int nu, void* work, int32_t* ids,
                 int32_t* status, otpu_stream_t stream);
 
+/* The reference's float64 emulation (opentpu/quant.py:895-1067), for checking model code
+ * against the operator:
+ *   otpu_fake_act: quant.fake_act of x [M, K] fp32 in ranges of n columns (K a multiple of n),
+ *   groups of g (16, 32 = QACT, 64, 128 = QST; row_mode: every offset 0): values v [M, K] float64
+ *   and da [M, K/16] (each 16-element group's offset).
+ *   otpu_dequant: quant.dequantize_mxu (values [N, K] float64, exact) and quant.group_offsets
+ *   (dw [N, K/16]) of element rows and scale rows (rsc: scale rows of Sw alone).
+ *   otpu_mx_matmul: quant.mx_matmul: y [M, N] float64 = h [M, K] @ w [N, K]^T over the
+ *   16-element groups MM's window W keeps (da[j, g] + dw[n, g] <= W; da NULL: every group;
+ *   dw NULL: offsets 0; dw_rows 1: one offset row for every n). */
+int otpu_fake_act(const float* x, int M, int K, int64_t ldx, int n, int g, int row_mode, double* v,
+                  int64_t ldv, uint8_t* da, int64_t ldda, otpu_stream_t stream);
+int otpu_dequant(const uint8_t* rows, int64_t rs, const uint8_t* srows, int64_t srs, int N, int K, int fmt,
+                 int rsc, double* out, int64_t ldo, uint8_t* dw, int64_t lddw, otpu_stream_t stream);
+int otpu_mx_matmul(const double* h, int64_t ldh, const uint8_t* da, int64_t ldda, const double* w,
+                   int64_t ldw, const uint8_t* dw, int64_t lddw, int dw_rows, int W, int M, int N, int K,
+                   double* y, int64_t ldy, otpu_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

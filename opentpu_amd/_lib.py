@@ -42,6 +42,9 @@ SIGNATURES = {
     "otpu_import_nvfp4": ([_P, _L, _P, _L, _F, _I, _I, _P, _L, _P, _L, _P, _P], _I),
     "otpu_sample_work_bytes": ([_I], _L),
     "otpu_sample": ([_P, _I, _P, _P, _D, _I, _F, _F, _P, _I, _P, _P, _P, _P], _I),
+    "otpu_fake_act": ([_P, _I, _I, _L, _I, _I, _I, _P, _L, _P, _L, _P], _I),
+    "otpu_dequant": ([_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P], _I),
+    "otpu_mx_matmul": ([_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P, _L, _P], _I),
 }
 
 
@@ -95,7 +98,7 @@ def ptr(t):
 
 
 _NP2T = {np.float32: "float32", np.int8: "int8", np.uint8: "uint8", np.int64: "int64",
-         np.int32: "int32", np.uint64: "uint64"}
+         np.int32: "int32", np.uint64: "uint64", np.float64: "float64"}
 
 
 def dev(x, dtype):
