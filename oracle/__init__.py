@@ -15,6 +15,7 @@ Modules
            ACC / ASCALE / RMAX; ARGMAX and greedy selection.
   groups   the reference machine's grouped / channel-hashed weight images (WG lanes) and their
            inverses, built byte address by byte address from the layout's formulas.
+  emulate  the reference's float64 emulation: fake_act, group offsets, mx_matmul's drops.
   imports  MXFP4 / NVFP4 checkpoint imports into fp4 / nvfp4 rows, exactly (NotExact).
   sampler  the sampled pick after the LM head: penalty, soft cap, knock-out top-k, the
            machine's exp2 softmax, top-p and the inverse-CDF pick.
