@@ -385,6 +385,11 @@ def main():
         extra["c3_gemm_row_x_rsc"] = {"us": round(ms3 * 1e3, 2), "TOPS": round(tops, 2),
                                       "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         print(f"[c3] {extra['c3_gemm_row_x_rsc']}", file=sys.stderr, flush=True)
+        # yardstick: writing c3's fp32 output alone (a fill kernel over the same 16.8 MB)
+        o3 = torch.empty((512, 8192), dtype=torch.float32, device="cuda")
+        msf = timed(lambda: o3.fill_(1.0), 20, 2, torch.cuda.current_stream())
+        del o3
+        extra["c3_output_write_alone"] = {"us": round(msf * 1e3, 2), "what": "torch fill_ of the 512 x 8192 fp32 output"}
     if "c3" in only:
         ms3m = gemm(5, 1, row_mode=False)
         tops = 2 * 512 * 2048 * 8192 / (ms3m * 1e-3) / 1e12

@@ -38,11 +38,12 @@ struct MMArgs {
 constexpr int QIN_KMAX = 4096;     // columns a prologue QACT holds in LDS
 constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds
 
-// rows a team takes per iteration: 16 rows' loads in flight per wave for one activation row
-// with one piece a lane (measured best on MI355X: 8 gave 3% less, 32 no more); 8 a team with four
-// or more pieces a lane (the LM head: 4% over 2); fewer as activation rows add sums to carry
+// rows a team takes per iteration: 8 rows' loads in flight per wave for one activation row
+// with one piece a lane (measured on MI355X: 16 the same for the 80-problem launches, 8 faster
+// for small grids), 4 when that still leaves CUs idle (R_SMALL); 8 a team with four or more
+// pieces a lane (the LM head: 4% over 2); fewer as activation rows add sums to carry
 #ifndef OTPU_GEMV_R1
-#define OTPU_GEMV_R1 16
+#define OTPU_GEMV_R1 8
 #endif
 #ifndef OTPU_GEMV_NT
 #define OTPU_GEMV_NT 1

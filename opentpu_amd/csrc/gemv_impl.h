@@ -264,10 +264,9 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
 
 // the kernel body for a team of T lanes (T a compile-time constant: the exchanges of the
 // reduction are then straight-line code); QIN: the activation row is quantized in the prologue
-template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN = false>
+template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN, int R>
 __device__ __forceinline__ void gemv_body(const MMArgs& a) {
     constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
-    constexpr int R = rows_per_team<L, MR>();
     constexpr int E = R * MR;                             // sums a lane carries per iteration
     static_assert(E <= T, "a team holds its E sums after the reduce-scatter");
     const int lane = threadIdx.x & 63;
@@ -450,19 +449,20 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a) {
     }
 }
 
-template <int FMT, int MR, int L, bool PLAIN>
+// R: rows a team takes per iteration
+template <int FMT, int MR, int L, bool PLAIN, int R>
 __global__ __launch_bounds__(256) void gemv_kernel(MMArgs a) {
-    if (a.T == 64) gemv_body<FMT, MR, L, 64, PLAIN>(a);
-    else if (a.T == 32) gemv_body<FMT, MR, L, 32, PLAIN>(a);
-    else gemv_body<FMT, MR, L, 16, PLAIN>(a);
+    if (a.T == 64) gemv_body<FMT, MR, L, 64, PLAIN, false, R>(a);
+    else if (a.T == 32) gemv_body<FMT, MR, L, 32, PLAIN, false, R>(a);
+    else gemv_body<FMT, MR, L, 16, PLAIN, false, R>(a);
 }
 
 // MM with the QACT of its one activation row in the prologue
-template <int FMT, int L, bool PLAIN>
+template <int FMT, int L, bool PLAIN, int R>
 __global__ __launch_bounds__(256) void gemv_qin_kernel(MMArgs a) {
-    if (a.T == 64) gemv_body<FMT, 1, L, 64, PLAIN, true>(a);
-    else if (a.T == 32) gemv_body<FMT, 1, L, 32, PLAIN, true>(a);
-    else gemv_body<FMT, 1, L, 16, PLAIN, true>(a);
+    if (a.T == 64) gemv_body<FMT, 1, L, 64, PLAIN, true, R>(a);
+    else if (a.T == 32) gemv_body<FMT, 1, L, 32, PLAIN, true, R>(a);
+    else gemv_body<FMT, 1, L, 16, PLAIN, true, R>(a);
 }
 
 // workgroups per CU the streaming grid aims for: 16 for one piece a lane and for four or more
@@ -477,22 +477,42 @@ inline int gemv_blocks_per_cu(int L) {
     return v ? v : ((L == 1 || L >= 4) ? 16 : 8);
 }
 
+// rows a team takes per iteration (one activation row, one piece a lane) when the default
+// would give fewer workgroups than CUs: a small single GEMV then still spreads over the chip
+constexpr int R_SMALL = 4;
+
+// the grid of a launch with R rows a team: about gemv_blocks_per_cu workgroups per CU over the
+// whole batch, fewer when the rows run out (each wave then streams many row groups; its
+// activation registers are loaded once)
+inline int64_t gemv_blocks(const MMArgs& a, int R, int L, int batch) {
+    const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
+    int64_t blocks = (waves + 3) / 4;
+    int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L) / batch;
+    if (cap < 1) cap = 1;
+    return blocks > cap ? cap : blocks;
+}
+
+template <int FMT, int MR, int L, int R>
+void launch_grid(const MMArgs& a, int batch, hipStream_t s) {
+    const int64_t blocks = gemv_blocks(a, R, L, batch);
+    if (a.flags & (OTPU_UNIT | OTPU_RSC))
+        gemv_kernel<FMT, MR, L, true, R><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+    else
+        gemv_kernel<FMT, MR, L, false, R><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+}
+
 template <int FMT, int MR, int L>
 void launch_one(const MMArgs& a, int batch, hipStream_t s) {
     static_assert(fits<FMT, 1, L>(), "one activation row always fits");
     if constexpr (fits<FMT, MR, L>()) {
         constexpr int R = rows_per_team<L, MR>();
-        const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
-        // about 8 resident workgroups per CU over the whole batch; each wave then streams
-        // many row groups (its activation registers are loaded once)
-        int64_t blocks = (waves + 3) / 4;
-        int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L) / batch;
-        if (cap < 1) cap = 1;
-        if (blocks > cap) blocks = cap;
-        if (a.flags & (OTPU_UNIT | OTPU_RSC))
-            gemv_kernel<FMT, MR, L, true><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
-        else
-            gemv_kernel<FMT, MR, L, false><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+        if constexpr (MR == 1 && L == 1 && R > R_SMALL) {
+            if (gemv_blocks(a, R, L, batch) * batch < otpu_cu_count()) {
+                launch_grid<FMT, MR, L, R_SMALL>(a, batch, s);
+                return;
+            }
+        }
+        launch_grid<FMT, MR, L, R>(a, batch, s);
     }
 }
 
@@ -516,18 +536,25 @@ void launch_fmt(const MMArgs& a, int mr, int L, int batch, hipStream_t s) {
     else launch_L<FMT, 4>(a, L, batch, s);
 }
 
+template <int FMT, int L, int R>
+void launch_qin_grid(const MMArgs& a, int batch, hipStream_t s) {
+    const int64_t blocks = gemv_blocks(a, R, L, batch);
+    if (a.flags & (OTPU_UNIT | OTPU_RSC))
+        gemv_qin_kernel<FMT, L, true, R><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+    else
+        gemv_qin_kernel<FMT, L, false, R><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+}
+
 template <int FMT, int L>
 void launch_qin(const MMArgs& a, int batch, hipStream_t s) {
     constexpr int R = rows_per_team<L, 1>();
-    const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
-    int64_t blocks = (waves + 3) / 4;
-    int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L) / batch;
-    if (cap < 1) cap = 1;
-    if (blocks > cap) blocks = cap;
-    if (a.flags & (OTPU_UNIT | OTPU_RSC))
-        gemv_qin_kernel<FMT, L, true><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
-    else
-        gemv_qin_kernel<FMT, L, false><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
+    if constexpr (L == 1 && R > R_SMALL) {
+        if (gemv_blocks(a, R, L, batch) * batch < otpu_cu_count()) {
+            launch_qin_grid<FMT, L, R_SMALL>(a, batch, s);
+            return;
+        }
+    }
+    launch_qin_grid<FMT, L, R>(a, batch, s);
 }
 
 template <int FMT>

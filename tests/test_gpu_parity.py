@@ -282,6 +282,9 @@ GEMM_CASES = [  # M, N, K, weights (rsc | int8x | unit), activations (row | mx |
     (96, 160, 256, "unit", "mx", 0),
     (128, 128, 2048, "rsc", "wide", 0),      # offsets over > 6 binades: the VALU tiles
     (40, 70, 640, "int8x", "wide", 1),       # drops (d + e > 16) inside the planes
+    (200, 300, 1024, "rsc", "row", 0),       # single plane, ragged tiles
+    (72, 136, 640, "unit", "row", 0),        # single plane, an odd number of K stages
+    (16, 16, 128, "rsc", "row", 0),          # single plane, one K stage
 ]
 
 
@@ -323,6 +326,13 @@ def test_gemm_acc_ascale(ops):
     old = rng.standard_normal((M, N)).astype(np.float32)
     alpha = rng.standard_normal(M).astype(np.float32)
     say("gemm acc / ascale")
+    got = mxu.mm(q, Sa, da, wel, srows, "int8", K, unit=True, acc=old)
+    assert same_bits(got, OC.mm(q, Sa, da, wel, srows, "int8", K, flags=MM.UNIT | MM.ACC, old=old))
+    got = mxu.mm(q, Sa, da, wel, srows, "int8", K, unit=True, acc=old, alpha=alpha)
+    assert same_bits(got, OC.mm(q, Sa, da, wel, srows, "int8", K, flags=MM.UNIT | MM.ACC | MM.ASCALE,
+                                old=old, alpha=alpha))
+    # ROW activations: the single-plane path's epilogue
+    q, Sa, da = F.quantize_mx(x, 32, row_mode=True)
     got = mxu.mm(q, Sa, da, wel, srows, "int8", K, unit=True, acc=old)
     assert same_bits(got, OC.mm(q, Sa, da, wel, srows, "int8", K, flags=MM.UNIT | MM.ACC, old=old))
     got = mxu.mm(q, Sa, da, wel, srows, "int8", K, unit=True, acc=old, alpha=alpha)
