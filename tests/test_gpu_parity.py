@@ -274,6 +274,44 @@ def test_batched_is_independent_mms(ops):
         assert same_bits(got[b], want[b])
 
 
+@pytest.mark.parametrize("fmt,rsc", [("int8", True), ("int8", False), ("int4", False), ("fp4", False)])
+def test_gemv_row_blocking_paths(ops, fmt, rsc):
+    """One launch of 32 problems (a grid over every CU: 8 rows a team) and the same problems
+    one launch each (a small grid: 4 rows a team), both against the C oracle."""
+    import torch
+    _, _, mxu = ops
+    from opentpu_amd import _lib as X
+    rng = np.random.default_rng(31 + len(fmt) + rsc)
+    B, N, K = 32, 512, 1024
+    qs, Sas, das, rs, ss, want = [], [], [], [], [], []
+    flags = MM.RSC if rsc else 0
+    for b in range(B):
+        W = (spread(rng, N, K, 1.5, 128) * 0.02).astype(np.float32)
+        x = spread(rng, 1, K, 2.0, 32)
+        if fmt == "int8":
+            r, sr = Q.pack_rsc(W) if rsc else Q.pack_int8x(W)
+        else:
+            r, sr = Q.pack_x4(W, fmt)
+        q, Sa, da = F.quantize_mx(x, 32)
+        qs.append(q); Sas.append(Sa); das.append(da); rs.append(r); ss.append(sr)
+        want.append(OC.mm(q, Sa, da, r, sr, fmt, K, flags=flags))
+    qd = torch.from_numpy(np.concatenate(qs)).cuda()
+    Sad = torch.from_numpy(np.concatenate(Sas)).cuda()
+    dad = torch.from_numpy(np.concatenate(das)).cuda()
+    rd = torch.from_numpy(np.concatenate(rs)).cuda()
+    sd = torch.from_numpy(np.concatenate(ss)).cuda()
+    out = torch.empty((B, 1, N), dtype=torch.float32, device="cuda")
+    say("gemv row blocking", fmt, rsc)
+    X.call("otpu_mm_batched", B, X.ptr(qd), K, K, X.ptr(Sad), 1, X.ptr(dad), K // 32, K // 32, 1, K,
+           X.ptr(rd), rd.shape[1], N * rd.shape[1], X.ptr(sd), sd.shape[1], N * sd.shape[1], N, X.FMT[fmt],
+           flags, 0, X.ptr(out), N, N, X.stream())
+    got = out.cpu().numpy()
+    for b in range(B):
+        assert same_bits(got[b], want[b])
+        one = mxu.mm(qs[b], Sas[b], das[b], rs[b], ss[b], fmt, K, rsc=rsc)
+        assert same_bits(one, want[b])
+
+
 GEMM_CASES = [  # M, N, K, weights (rsc | int8x | unit), activations (row | mx | wide), k0
     (512, 384, 2048, "rsc", "row", 0),
     (200, 300, 1024, "rsc", "mx", 0),
