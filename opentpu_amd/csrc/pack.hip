@@ -10,9 +10,9 @@
 //   for f in linspace(0.64, 1.12, 13): m = clip(rint(sb / unit * f), 1, 63), s = unit * m,
 //     err = sum((grid(x / s) * s - x)^2) in numpy's pairwise order (8 running partials,
 //     ((p0+p1)+(p2+p3))+((p4+p5)+(p6+p7))); the first strictly smaller err wins.
-// floor(log2(v)) is taken exactly from v's exponent; numpy's rounded log2 can differ only for
-// v within a few ulps below a power of two >= 4 (never reached by a block holding the row's
-// largest sub-block, whose v is within 2^-24 of 1).
+// floor(log2(v)) is taken exactly from v's exponent. numpy's rounded log2 agrees for every
+// float32 input: 63 qmax Sw has at most 33 significant bits and bmax = rnd(a / qmax) for a
+// float32 a, so v is a power of two or at least ~2^-34 (relative) away from every one.
 #include <cmath>
 
 #include "otpu_common.h"

@@ -163,3 +163,39 @@ def test_nv_packer_layout_and_error():
     deq = Q.dequantize(rows, srows, "nvfp4", 384)
     err = np.abs(deq - W.astype(np.float64))
     assert err.max() <= np.abs(W).max() / 6 + 1e-12             # within an E2M1 step of amax
+
+
+@pytest.mark.parametrize("fmt,qmax", [("int4", 7.0), ("fp4", 6.0)])
+def test_packer_block_offset_log2_is_exact(fmt, qmax):
+    """The 4-bit packers' block offset floor(log2(v)), v = 63 Sw / bmax in float64: numpy's
+    rounded log2 (the reference) and the exponent of v (the GPU packer) agree because v is
+    either a power of two or at least ~2^-34 (relative) away from every one: 63 qmax Sw has at
+    most 33 significant bits and bmax = rnd(a / qmax) for a float32 a. Checked here on random
+    rows, rows whose block maxima differ by powers of two, and the 441 * 2^k family that makes
+    v exactly a power of two."""
+    import math
+    rng = np.random.default_rng(17)
+    rows = [_spread(rng, 64, 1024, 2.0)]
+    base = rng.standard_normal((64, 1024)).astype(np.float32)
+    pw = np.exp2(rng.integers(-12, 1, (64, 8, 1))).astype(np.float32)
+    rows.append((base.reshape(64, 8, 128) * 0 + pw * np.float32(0.5)).reshape(64, 1024).astype(np.float32))
+    fam = np.zeros((8, 1024), np.float32)
+    for r in range(8):
+        fam[r, ::128] = np.float32(qmax * 63.0) * np.exp2(-np.arange(8) - r).astype(np.float32)
+    rows.append(fam)
+    gap_min, exact = 1.0, 0
+    for W in rows:
+        x = W.astype(np.float64).reshape(W.shape[0], -1, 4, 32)
+        sb = np.abs(x).max(-1) / qmax
+        top = sb.max(-1).max(-1)
+        Sw = np.where(top == 0, 1.0, top / 63).astype(np.float32).astype(np.float64)
+        bmax = sb.max(-1)
+        ok = bmax > 0
+        v = (63 * Sw[:, None] / np.where(ok, bmax, 1.0))[ok]
+        e = np.array([math.frexp(t)[1] - 1 for t in v])
+        assert np.array_equal(np.floor(np.log2(v)).astype(np.int64), e)
+        rel = v / np.exp2(np.round(np.log2(v))) - 1.0
+        exact += int((rel == 0).sum())
+        gap_min = min(gap_min, float(np.abs(rel[rel != 0]).min()) if np.any(rel != 0) else 1.0)
+    print(fmt, "exact powers of two:", exact, "smallest relative gap:", gap_min)
+    assert exact > 0 and gap_min > 2.0 ** -36
