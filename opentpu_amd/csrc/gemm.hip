@@ -345,6 +345,81 @@ __device__ __forceinline__ void gemm_pass_ring(const GemmArgs& a, int8_t* ring, 
     ring_barrier();
 }
 
+// Several activation planes in one K walk (plain weights: every dw = 0, so plane s = d): the
+// ring and its direct loads as in gemm_pass_ring, and each stage's A fragments multiplied once
+// per plane, masked to the 32-groups whose offset is that plane's d (groups of no listed plane,
+// e.g. offsets past the window, are dropped).  The planes' products go to separate int32
+// accumulators, combined after the walk: acc = sum_p C_p << (smax - d_p), Horner's sum unrolled.
+// The group offsets of the tile come from LDS (da_lds: row r's word of stage kt at r * DAS + kt,
+// four offsets a word, staged by the offset scan).  One pass of loads serves every plane.
+constexpr int MP_MAX = 3;                       // planes one walk carries (64 registers of sums each;
+                                                // 4 spill)
+constexpr int MP_KT = 32;                       // stages (K = 4096) the staged offsets cover
+constexpr int DAS = MP_KT + 1;                  // their row stride in words (16 rows on 16 banks)
+
+template <int NP>
+__device__ __forceinline__ void gemm_pass_mp(const GemmArgs& a, int8_t* ring, const uint32_t* da_lds,
+                                             v4i (&acc)[MP_MAX][4][4], const int (&dv)[MP_MAX], int m0, int n0) {
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wid >> 1, wn = wid & 1;
+    const RingSrc rs = ring_src(a, ring, m0, n0);
+    const int KS = a.K / RBK;
+    constexpr int KSTEP = RBK / 64;
+    constexpr int EVERY = 16 * KSTEP * NP / LPS;          // MFMAs per refill load
+    static_assert(RBK == 128, "offset words cover 128-byte stages");
+    for (int kt = 0; kt < KS; ++kt) {
+        wait_stage(min(NS - 2, KS - 1 - kt));
+        ring_barrier();
+        const int8_t* A = ring + (kt % NS) * STAGE;
+        const int8_t* B = A + TILE;
+        v4i fa[KSTEP][4], fb[KSTEP][4];
+        uint32_t dw4[4];                                   // this lane's rows' offset words
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dw4[i] = da_lds[(wm * 64 + i * 16 + (lane & 15)) * DAS + kt];
+#pragma unroll
+        for (int ks = 0; ks < KSTEP; ++ks) {
+            const int c = ks * 4 + (lane >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fa[ks][i] = *reinterpret_cast<const v4i*>(A + rof(wm * 64 + i * 16 + (lane & 15), c));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[ks][j] = *reinterpret_cast<const v4i*>(B + rof(wn * 64 + j * 16 + (lane & 15), c));
+        }
+        const int nk = kt + NS - 1;
+        const bool refill = nk < KS;
+        const uint32_t sl = rs.base + (uint32_t)((nk % NS) * STAGE);
+        const int o = nk * RBK;
+#pragma unroll
+        for (int ks = 0; ks < KSTEP; ++ks) {
+            // the 16 bytes at chunk c are 32-group c >> 1 of the stage: offset byte (c >> 1)
+            const int gsh = 8 * ((ks * 4 + (lane >> 4)) >> 1);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                v4i fm[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool keep = ((dw4[i] >> gsh) & 0xFFu) == (uint32_t)dv[p];
+                    fm[i] = keep ? fa[ks][i] : v4i{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fm[i], fb[ks][j], acc[p][i][j], 0, 0, 0);
+                        const int x = (ks * NP + p) * 16 + i * 4 + j;
+                        if (x % EVERY == EVERY - 1 && refill) {
+                            const int u = x / EVERY;
+                            __builtin_amdgcn_sched_barrier(0);
+                            if (u < LPS / 2) dma16(rs.ga[u] + o, sl + 1024u * u);
+                            else dma16(rs.gb[u - LPS / 2] + o, sl + TILE + 1024u * (u - LPS / 2));
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+            }
+        }
+    }
+    ring_barrier();
+}
+
 // A full tile leaves through LDS: each wave writes its 64 x 64 values in the MFMA layout (rows
 // 68 floats apart: the 4 row groups of a write land on distinct banks) and reads them back as
 // float4 rows, so every store instruction writes 4 rows x 256 contiguous bytes.  `lds` is the
@@ -444,6 +519,41 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int8_t* lds, in
         }
 }
 
+// a tile of plain weights whose activation groups hold NP offsets d (planes s = d): one K walk
+// (gemm_pass_mp), the planes' sums combined, then the epilogue
+template <int NP>
+__device__ __forceinline__ void gemm_tile_mp(const GemmArgs& a, int8_t* ring, const uint32_t* da_lds, int m0, int n0,
+                                             uint32_t dmask, int smax, const float (&sw)[4], const float (&sa2)[4][4]) {
+    int dv[MP_MAX];
+    uint32_t left = dmask;
+#pragma unroll
+    for (int p = 0; p < MP_MAX; ++p) {               // the planes' d in ascending order
+        dv[p] = left ? __builtin_ctz(left) : 255;
+        left &= left - 1;
+    }
+    v4i acc[MP_MAX][4][4];
+#pragma unroll
+    for (int p = 0; p < MP_MAX; ++p)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[p][i][j] = v4i{0, 0, 0, 0};
+    gemm_pass_mp<NP>(a, ring, da_lds, acc, dv, m0, n0);
+    // sum_p C_p << (smax - d_p) = C << (16 - smax) with C an int32 (the bound checked by the caller)
+    float v[4][4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v4i t = acc[0][i][j] << (smax - dv[0]);
+#pragma unroll
+            for (int p = 1; p < NP; ++p) t += acc[p][i][j] << (smax - dv[p]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[i][j][e] = ldexpf((float)t[e], 16 - smax);
+        }
+    tile_epilogue(a, ring, m0, n0, v, sw, sa2);
+}
+
 // a tile's planes in ascending s (Horner in the int32 accumulators), then its epilogue
 template <bool MA, bool MB>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int m0, int n0, uint32_t dmask,
@@ -488,6 +598,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     __shared__ uint32_t sDa[2][GBM];       // the stage's four da bytes per activation row
     __shared__ uint8_t sDw[2][GBN];        // the stage's dw byte per weight row
     __shared__ uint32_t sMask[8];          // per wave: d values and e values present in the tile
+    __shared__ uint32_t sDaAll[GBM * DAS]; // the tile's offset words (K <= 4096), for gemm_pass_mp
 
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wid >> 1, wn = wid & 1;
@@ -537,6 +648,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
 #pragma unroll 8
             for (int k = h; k < KT; k += 2) {                 // K / 128 words of four offsets
                 const uint32_t wd = drow[k];
+                if (KT <= MP_KT) sDaAll[r * DAS + k] = wd;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const uint32_t d = (wd >> (8 * t)) & 0xFF;
@@ -621,6 +733,16 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
                   reinterpret_cast<int8_t(*)[GBN * GBK]>(sRing + 2 * GBM * GBK), sDa, sDw, sRing};
     if (single) {
         gemm_tile<false, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
+        return;
+    }
+    // plain weights, up to MP_MAX activation planes: one K walk through the ring for all of them
+    const int np = __builtin_popcount(dmask);
+    if (plain && KT <= MP_KT && np >= 1 && np <= MP_MAX) {
+        switch (np) {
+            case 1: gemm_tile_mp<1>(a, sRing, sDaAll, m0, n0, dmask, smax, sw, sa2); break;
+            case 2: gemm_tile_mp<2>(a, sRing, sDaAll, m0, n0, dmask, smax, sw, sa2); break;
+            default: gemm_tile_mp<3>(a, sRing, sDaAll, m0, n0, dmask, smax, sw, sa2); break;
+        }
         return;
     }
     wait_dma<0>();                                  // the masked passes reuse the ring's memory

@@ -353,6 +353,26 @@ def test_gemm(ops, M, N, K, wk, ak, k0):
     assert same_bits(got, want)
 
 
+@pytest.mark.parametrize("dset", [(0, 1), (0, 1, 2), (1, 3, 4), (0, 1, 2, 3), (0, 20), (2, 5, 17), (0, 31)])
+def test_gemm_activation_planes(ops, dset):
+    """Plain (RSC) weights x activation groups whose offsets take the values dset: one to three
+    planes in one K walk, four planes in the plane-by-plane passes, offsets past the window
+    (dropped); against the C oracle."""
+    import torch
+    _, _, mxu = ops
+    rng = np.random.default_rng(sum(dset) * 7 + len(dset))
+    M, N, K = 200, 256, 1024
+    q = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    Sa = np.abs(rng.standard_normal(M)).astype(np.float32) + np.float32(0.5)
+    da = np.asarray(dset, np.uint8)[rng.integers(0, len(dset), (M, K // 32))]
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    rows, srows = Q.pack_rsc(W)
+    say("gemm planes", dset)
+    got = mxu.mm(q, Sa, da, rows, srows, "int8", K, rsc=True)
+    want = OC.mm(q, Sa, da, rows, srows, "int8", K, flags=MM.RSC)
+    assert same_bits(got, want)
+
+
 def test_gemm_acc_ascale(ops):
     _, _, mxu = ops
     rng = np.random.default_rng(9)
