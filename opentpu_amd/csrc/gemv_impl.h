@@ -465,8 +465,10 @@ __global__ __launch_bounds__(256) void gemv_qin_kernel(MMArgs a) {
     else gemv_body<FMT, 1, L, 16, PLAIN, true, R>(a);
 }
 
-// workgroups per CU the streaming grid aims for: 16 for one piece a lane and for four or more
-// (the LM head: 4% over 8), else 8 (measured on MI355X); OTPU_GEMV_BLOCKS_PER_CU overrides
+// workgroups per CU the streaming grid aims for (measured on MI355X): 32 for one piece a lane
+// (the 80-problem c2: 6.61 TB/s against 6.36 at 16 and 6.48 at 64; each wave then streams one
+// or two row groups, so the last round of workgroups is short), 16 for four or more (the LM
+// head: the same from 16 to 64, 4% over 8), else 8; OTPU_GEMV_BLOCKS_PER_CU overrides
 inline int gemv_blocks_per_cu(int L) {
     static int v = -1;
     if (v < 0) {
@@ -474,7 +476,7 @@ inline int gemv_blocks_per_cu(int L) {
         int x = e ? atoi(e) : 0;
         v = (x > 0 && x <= 64) ? x : 0;
     }
-    return v ? v : ((L == 1 || L >= 4) ? 16 : 8);
+    return v ? v : (L == 1 ? 32 : (L >= 4 ? 16 : 8));
 }
 
 // rows a team takes per iteration (one activation row, one piece a lane) when the default
