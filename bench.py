@@ -209,7 +209,7 @@ def c4_step(steps, warmup):
         it[0] += 1
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
     wb = sh.layers * sh.layer_bytes("int4")
-    launches = sh.layers * DecodeChain.FUSED_KERNELS_PER_LAYER + 1
+    launches = chains[0].kernels_per_step
     del chains
     torch.cuda.empty_cache()
     return {"us_per_step": round(ms * 1e3, 2), "weight_bytes": wb, "GBps": round(wb / (ms * 1e-3) / 1e9, 1),

@@ -116,6 +116,18 @@ int otpu_mm_qin(const float* x, const float* xmul, int nsum, int64_t sum_stride,
                 const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
                 int k0, float* out, int64_t ors, int64_t part_stride, otpu_stream_t stream);
 
+/* The chained layer's down projection folded in one launch (Builder.dot's per-range MMs with
+ * their ACC, opentpu/compiler.py:2686-2720; swiglu_down's chunk loop,
+ * opentpu/kernels/mlp.py:87-120): the fp32 row mul(x, xmul) (xmul may be NULL) in K / 256
+ * ranges of 256 columns (the 4-bit down chunk at F = 3072, opentpu/kernels/mlp.py:8-24), each
+ * quantized by its own QACT and multiplied by its weight columns, and the ranges' outputs added
+ * in range order into out[0..N): otpu_mm_qin's ranges and the fold of their rows, bit for bit.
+ * 4-bit weights with scale rows only (INT4, FP4, NVFP4; no flags but PAIR); K a multiple of 256,
+ * at most 4096. */
+int otpu_mm_qin_fold(const float* x, const float* xmul, int K, const uint8_t* w, int64_t rs,
+                     const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0, float* out,
+                     otpu_stream_t stream);
+
 /* The ACC fold of R rows of n (opentpu/isasim.py:899-905 applied in order): out = add(..add(
  * add(old | p_0, p_1)..), p_R-1) with FTZ adds, rows pstride apart; old may be NULL. */
 int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float* old, float* out,

@@ -35,6 +35,7 @@ SIGNATURES = {
     "otpu_mm_ranges": ([_P, _L, _P, _P, _L, _I, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P], _I),
     "otpu_vmul": ([_P, _P, _P, _L, _P], _I),
     "otpu_mm_qin": ([_P, _P, _I, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _L, _P], _I),
+    "otpu_mm_qin_fold": ([_P, _P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P], _I),
     "otpu_acc_rows": ([_P, _I, _L, _I, _P, _P, _P], _I),
     "otpu_ungroup_rows": ([_P, _I, _I, _I, _I, _L, _P, _L, _P], _I),
     "otpu_ungroup_scales": ([_P, _I, _I, _I, _I, _I, _P, _L, _P], _I),

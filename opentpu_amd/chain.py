@@ -61,9 +61,11 @@ class DecodeChain:
     """`layers`: per layer a dict name -> (rows, srows) device tensors (uint8).
 
     fused (default): a layer is four kernels, each linear an otpu_mm_qin (the QACT of its input
-    row in the GEMV's prologue); the down projection's per-chunk outputs stay partial and the
-    next layer's prologue folds them in chunk order (the ACC chain), the step's last fold is one
-    otpu_acc_rows.  Unfused: the nine kernels of `layer` (QACT, MM, .. one call each)."""
+    row in the GEMV's prologue).  With 4-bit weights and 256-column down chunks the down
+    projection is one otpu_mm_qin_fold, which folds its chunks' outputs in chunk order (the ACC
+    chain) itself; otherwise its per-chunk outputs stay partial, the next layer's prologue folds
+    them in chunk order and the step's last fold is one otpu_acc_rows.  Unfused: the nine
+    kernels of `layer` (QACT, MM, .. one call each)."""
 
     KERNELS_PER_LAYER = 9          # unfused: 3 QACT, 3 MM, QACT ranges, per-range MM + its ACC fold
     FUSED_KERNELS_PER_LAYER = 4    # fused: one QACT + MM kernel per linear
@@ -76,6 +78,9 @@ class DecodeChain:
         s = shape
         self.width = down_chunk(s.F, fmt)
         self.R = s.F // self.width
+        # the down projection folded in its own launch (4-bit, 256-column chunks); False keeps
+        # the per-chunk partial rows folded by the next layer's prologue
+        self.fold = fmt != "int8" and self.width == 256 and s.F <= 4096
         nq = s.q_dim + 2 * s.kv_dim
         T = X.torch()
         dev = "cuda"
@@ -92,6 +97,7 @@ class DecodeChain:
         self.da = T.empty((1, kmax // 32), dtype=u8, device=dev)
         self.part = T.empty((self.R, s.hidden), dtype=f32, device=dev)
         self.parts = [T.zeros((self.R, s.hidden), dtype=f32, device=dev) for _ in range(2)]
+        self.hbuf = [T.zeros((1, s.hidden), dtype=f32, device=dev) for _ in range(2)]
         self._graph = None
 
     @staticmethod
@@ -169,8 +175,33 @@ class DecodeChain:
         self._qin(w["gu"], self.o, s.hidden, s.hidden, self.gu)
         self._qin(w["down"], self.gu, s.F, self.width, parts, part_stride=s.hidden, xmul=self.gu[:, s.F:])
 
+    def layer_folded(self, l: int, x, y) -> None:
+        """Queue layer l fused, its down projection folded in one launch: input x [1, hidden] ->
+        output y [1, hidden]."""
+        s, w = self.shape, self.layers[l]
+        self._qin(w["qkv"], x, s.hidden, s.hidden, self.qkv)
+        self._qin(w["o"], self.qkv, s.q_dim, s.q_dim, self.o)
+        self._qin(w["gu"], self.o, s.hidden, s.hidden, self.gu)
+        rows, srows = w["down"]
+        X.call("otpu_mm_qin_fold", X.ptr(self.gu), X.ptr(self.gu[:, s.F:]), s.F, X.ptr(rows), rows.shape[1],
+               X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(y), X.stream())
+
+    @property
+    def kernels_per_step(self) -> int:
+        n = len(self.layers)
+        if not self.fused:
+            return n * self.KERNELS_PER_LAYER
+        return n * self.FUSED_KERNELS_PER_LAYER + (0 if self.fold else 1)  # + the last otpu_acc_rows
+
     def _queue(self) -> None:
         n = len(self.layers)
+        if self.fused and self.fold:
+            src = self.x
+            for l in range(n):
+                dst = self.y if l == n - 1 else self.hbuf[l % 2]
+                self.layer_folded(l, src, dst)
+                src = dst
+            return
         if self.fused:
             src, nsum = self.x, 1
             for l in range(n):

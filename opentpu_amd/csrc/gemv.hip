@@ -295,6 +295,34 @@ extern "C" int otpu_mm_qin(const float* x, const float* xmul, int nsum, int64_t 
     return otpu_launch_check("mm_qin");
 }
 
+namespace otpu {
+void launch_fold(const MMArgs& a, int fmt, int L, hipStream_t s);   // gemv_fold.hip
+}
+
+extern "C" int otpu_mm_qin_fold(const float* x, const float* xmul, int K, const uint8_t* w, int64_t rs,
+                                const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0, float* out,
+                                otpu_stream_t stream) {
+    if (fmt == OTPU_INT8) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: 4-bit weights (F-chunks of 256)");
+    if (flags & ~OTPU_PAIR) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: no flags (weights with scale rows)");
+    if (K < 256 || K % 256 || K > QIN_KMAX)
+        return otpu_fail(OTPU_EINVAL, "mm_qin_fold: K %d (a multiple of 256, at most %d)", K, QIN_KMAX);
+    if (!x || !out) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: x / out NULL");
+    if (!al(x, 16) || (xmul && !al(xmul, 16))) return otpu_fail(OTPU_EALIGN, "mm_qin_fold: x and xmul 16-byte aligned");
+    int rc = check_mm("mm_qin_fold", reinterpret_cast<const int8_t*>(x), K, reinterpret_cast<const uint8_t*>(x),
+                      K / 32, 1, K, w, rs, ws, srs, N, fmt, flags, k0);
+    if (rc) return rc;
+    if (rs < K / 2) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: rs %lld short of K %d", (long long)rs, K);
+    MMArgs a = make_args(nullptr, K, nullptr, nullptr, K / 32, 1, K, w, rs, ws, srs, N, flags & ~OTPU_PAIR, k0);
+    a.out = out; a.ors = N;
+    a.xin = x; a.xmul = xmul; a.nsum = 1;
+    a.P = (K / 2) / 16;
+    int L = 1;
+    pick_team(a.P, &a.T, &L);
+    if (L > 4) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: K %d needs %d pieces a lane (at most 4)", K, L);
+    launch_fold(a, fmt, L, (hipStream_t)stream);
+    return otpu_launch_check("mm_qin_fold");
+}
+
 extern "C" int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float* old, float* out,
                              otpu_stream_t stream) {
     if (!parts || !out || R < 1 || n < 1 || (R > 1 && pstride < n))

@@ -151,6 +151,37 @@ def test_mm_qin(X, fmt, K, width, nsum, mul):
         assert same_bits(got[r:r + 1], y), f"range {r}"
 
 
+@pytest.mark.parametrize("fmt,K,N", [("int4", 3072, 1024), ("int4", 1024, 300), ("fp4", 1536, 257),
+                                      ("nvfp4", 2048, 130), ("int4", 4096, 77)])
+def test_mm_qin_fold(X, fmt, K, N):
+    """The down projection folded in one launch: QACT of every 256-column range of mul(g, u), an
+    MM per range and the ACC of the ranges in order, against the oracle's ranges_dot."""
+    import torch
+    from oracle import formats as Q
+    rng = np.random.default_rng(K + N + len(fmt))
+    W = (spread(rng, N, K, 1.5, 128) * 0.02).astype(np.float32)
+    rows, srows = Q.quantize_mxu(W, fmt)
+    g, u = spread(rng, 1, K), spread(rng, 1, K)
+    want = CH.ranges_dot(F.mul(g, u), (rows, srows), fmt, 256)
+    say("mm_qin_fold", fmt, K, N)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    gd, ud, wd, sd = d(g), d(u), d(rows), d(srows)
+    out = torch.full((1, N), 7.0, dtype=torch.float32, device="cuda")
+    X.call("otpu_mm_qin_fold", X.ptr(gd), X.ptr(ud), K, X.ptr(wd), rows.shape[1], X.ptr(sd), srows.shape[1], N,
+           X.FMT[fmt], 0, 0, X.ptr(out), X.stream())
+    assert same_bits(out.cpu().numpy(), want)
+
+
+def test_mm_qin_fold_refusals(X):
+    from opentpu_amd._lib import OtpuError
+    p = 256
+    for args in [(1024, X.FMT["int8"], 0), (1000, X.FMT["int4"], 0), (8192, X.FMT["int4"], 0),
+                 (1024, X.FMT["int4"], X.RSC)]:
+        K, fmt, flags = args
+        with pytest.raises(OtpuError):
+            X.call("otpu_mm_qin_fold", p, p, K, p, 512, p, 40, 8, fmt, flags, 0, p, X.stream())
+
+
 def test_acc_rows(X):
     import torch
     rng = np.random.default_rng(9)
@@ -200,7 +231,14 @@ def test_chain_layers_small(X):
     ch.fused = False
     assert same_bits(ch.step(x).cpu().numpy(), want)
     ch.fused = True
+    assert ch.fold
     assert same_bits(ch.step(x).cpu().numpy(), want)
+    ch.fold = False                                # the down chunks' partial rows, folded later
+    assert same_bits(ch.step(x).cpu().numpy(), want)
+    ch.fold = True
+    yd = torch.empty((1, 256), dtype=torch.float32, device="cuda")
+    ch.layer_folded(1, torch.from_numpy(x).cuda(), yd)
+    assert same_bits(yd.cpu().numpy(), CH.layer(x, host[1], "int4", 512, 768)[0])
 
 
 def test_chain_c4_full_and_graph(X):
@@ -227,8 +265,12 @@ def test_chain_c4_full_and_graph(X):
     say("nonzero outputs per layer", nonzero)
     assert nonzero[0] > 900
     want = xo
-    say("chain c4: eager step, fused and unfused")
+    say("chain c4: eager step, fused (folded down projection, and partial rows) and unfused")
+    assert ch.fold and ch.kernels_per_step == 112
     assert same_bits(ch.step(x).cpu().numpy(), want)
+    ch.fold = False
+    assert same_bits(ch.step(x).cpu().numpy(), want)
+    ch.fold = True
     ch.fused = False
     assert same_bits(ch.step(x).cpu().numpy(), want)
     ch.fused = True
@@ -239,7 +281,10 @@ def test_chain_c4_full_and_graph(X):
         ch.layer_fused(l, ch.x, 1, ch.parts[0])
         yl = torch.empty((1, 1024), dtype=torch.float32, device="cuda")
         X.call("otpu_acc_rows", X.ptr(ch.parts[0]), ch.R, 1024, 1024, None, X.ptr(yl), X.stream())
-        assert same_bits(yl.cpu().numpy(), CH.layer(xl, host[l], "int4")[0]), f"fused layer {l}"
+        want_l = CH.layer(xl, host[l], "int4")[0]
+        assert same_bits(yl.cpu().numpy(), want_l), f"fused layer {l}"
+        ch.layer_folded(l, ch.x, yl)
+        assert same_bits(yl.cpu().numpy(), want_l), f"folded layer {l}"
     say("chain c4: graph")
     ch.capture()
     for i in range(3):
