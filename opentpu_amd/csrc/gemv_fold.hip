@@ -96,8 +96,8 @@ __device__ __forceinline__ void fold_body(const MMArgs& a) {
     }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
-        am[k] = dpp_max_u32(cm[k], 64);                  // the range's maximum
-        gm[k] = dpp_max_u32(cm[k], 8);                   // the 8 chunks of this 32-group
+        am[k] = wave_max_dpp(cm[k], 64);                  // the range's maximum
+        gm[k] = wave_max_dpp(cm[k], 8);                   // the 8 chunks of this 32-group
     }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {

@@ -165,23 +165,6 @@ __device__ __forceinline__ double xsum(double x, int o) {
     return x + (o == 8 ? dpp_partner<8>(x) : o == 4 ? dpp_partner<4>(x) : o == 2 ? dpp_partner<2>(x) : dpp_partner<1>(x));
 }
 
-// max of v over aligned groups of 8 lanes (width 8) or the whole wave (width 64), every lane
-// receiving it: DPP quad_perm swaps across lane bits 0 and 1, then row_half_mirror (lane i <->
-// 7 - i within 8) and row_mirror (i <-> 15 - i within 16) -- each pairs lanes of the two halves
-// already reduced -- then v_permlane16_swap / v_permlane32_swap across bits 4 and 5.  (A
-// __shfl_xor step is an LDS permute: ~10x the latency.)
-__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v, int width) {
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
-    if (width == 8) return v;
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
-    const auto p16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    v = max((uint32_t)p16[0], (uint32_t)p16[1]);
-    const auto p32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return max((uint32_t)p32[0], (uint32_t)p32[1]);
-}
-
 // QACT of the problem's fp32 row in the prologue (fp32.quantize_mx(x, 32) of one row, as
 // qact_kernel computes it), once per workgroup: each thread takes float4 chunks of the row
 // (folding nsum partial rows in order, times xmul when given), the workgroup finds the row
@@ -263,7 +246,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
         }
     }
     }
-    m = dpp_max_u32(m, 64);
+    m = wave_max_dpp(m, 64);
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
     const uint32_t amax = max(max(red[0], red[1]), max(red[2], red[3]));
@@ -276,7 +259,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
         if (k * 256 >= NC) break;                        // uniform: the shuffles below converge
         uint32_t gm = max(max(fbits(v[k].x) & 0x7FFFFFFFu, fbits(v[k].y) & 0x7FFFFFFFu),
                           max(fbits(v[k].z) & 0x7FFFFFFFu, fbits(v[k].w) & 0x7FFFFFFFu));
-        gm = dpp_max_u32(gm, 8);                         // the 8 chunks of this 32-group
+        gm = wave_max_dpp(gm, 8);                         // the 8 chunks of this 32-group
         int dg = 0;
         if (gm) {
             dg = (int)(amax >> 23) - (int)(gm >> 23) - ((gm & 0x7FFFFFu) > (amax & 0x7FFFFFu));

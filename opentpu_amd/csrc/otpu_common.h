@@ -117,6 +117,27 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v, int width) {
     return v;
 }
 
+// max of v over aligned groups of `width` lanes (2, 4, .., 64), every lane receiving it; every
+// lane of the wave must be active.  DPP quad_perm swaps cross lane bits 0 and 1, then
+// row_half_mirror (lane i <-> 7 - i within 8) and row_mirror (i <-> 15 - i within 16) -- each
+// pairs lanes of two halves already reduced -- then v_permlane16_swap / v_permlane32_swap cross
+// bits 4 and 5.  A __shfl_xor step (wave_max_u32) is an LDS permute, ~10x the latency.
+__device__ __forceinline__ uint32_t wave_max_dpp(uint32_t v, int width) {
+    if (width >= 2) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+    if (width >= 4) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+    if (width >= 8) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+    if (width >= 16) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+    if (width >= 32) {
+        const auto p16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        v = max((uint32_t)p16[0], (uint32_t)p16[1]);
+    }
+    if (width >= 64) {
+        const auto p32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        v = max((uint32_t)p32[0], (uint32_t)p32[1]);
+    }
+    return v;
+}
+
 }  // namespace otpu
 
 // host-side error reporting shared by the entry points (abi.hip)

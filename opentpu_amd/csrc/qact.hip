@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void qact_kernel(const float* __restrict__ x, 
         m = max(m, fbits(ftz(v.z)) & 0x7FFFFFFFu);
         m = max(m, fbits(ftz(v.w)) & 0x7FFFFFFFu);
     }
-    m = wave_max_u32(m, 64);
+    m = wave_max_dpp(m, 64);
     if ((lane & 63) == 0) red[lane >> 6] = m;
     __syncthreads();
     const uint32_t amax = max(max(red[0], red[1]), max(red[2], red[3]));
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void qact_kernel(const float* __restrict__ x, 
         if (GL > 0) {
             uint32_t gm = max(max(fbits(ftz(v.x)) & 0x7FFFFFFFu, fbits(ftz(v.y)) & 0x7FFFFFFFu),
                               max(fbits(ftz(v.z)) & 0x7FFFFFFFu, fbits(ftz(v.w)) & 0x7FFFFFFFu));
-            gm = wave_max_u32(gm, GL);
+            gm = wave_max_dpp(gm, GL);
             if (gm) {
                 dg = (int)(amax >> 23) - (int)(gm >> 23) - ((gm & 0x7FFFFFu) > (amax & 0x7FFFFFu));
                 dg = dg < 0 ? 0 : (dg > 31 ? 31 : dg);
