@@ -151,11 +151,6 @@ def lm_head(steps, warmup):
         X.call("otpu_lm_head_argmax", X.ptr(q), X.ptr(Sa), X.ptr(da), K, X.ptr(rows), K, X.ptr(srows), 4, N,
                X.FMT["int8"], X.RSC, 0, 0, X.ptr(logits), X.ptr(best), X.ptr(tok), X.stream())
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
-
-    def step_qin():                                # the hidden row's QACT in the same launch
-        X.call("otpu_lm_head_argmax_qin", X.ptr(x), K, X.ptr(rows), K, X.ptr(srows), 4, N, X.FMT["int8"], X.RSC, 0,
-               0, X.ptr(logits), X.ptr(best), X.ptr(tok), X.stream())
-    ms_qin = timed(step_qin, steps, warmup, torch.cuda.current_stream())
     # the sampled pick after the same LM head: V = 262144, top-k 50, top-p 0.9, penalty 1.1 over
     # a 64-token context, one uniform (the sampler alone, then LM head + sampler in one graph)
     from opentpu_amd import sampler as SM
@@ -171,7 +166,7 @@ def lm_head(steps, warmup):
         pick()
     ms_both = timed(both, steps, warmup, torch.cuda.current_stream())
     sm.check()
-    return ms, int(tok.item()), ms_pick, ms_both, ms_qin
+    return ms, int(tok.item()), ms_pick, ms_both
 
 
 def gemm(steps, warmup, row_mode=True):
@@ -373,11 +368,10 @@ def main():
         torch.cuda.empty_cache()
         print(f"[c1] {extra['c1_int8_rsc_gemv']}", file=sys.stderr, flush=True)
     if "c5" in only:
-        ms5, tok, ms_pick, ms_both, ms_qin = lm_head(10, 2)
+        ms5, tok, ms_pick, ms_both = lm_head(10, 2)
         extra["c5_lm_head_argmax"] = {"us": round(ms5 * 1e3, 2), "token": tok,
                                       "GBps": round(c5_bytes() / (ms5 * 1e-3) / 1e9, 1),
-                                      "frac_hbm": round(c5_bytes() / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                      "with_qact_in_launch_us": round(ms_qin * 1e3, 2)}
+                                      "frac_hbm": round(c5_bytes() / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         extra["c5_sampler"] = {"pick_us": round(ms_pick * 1e3, 2), "lm_head_plus_pick_us": round(ms_both * 1e3, 2),
                                "sampling": "top_k 50, top_p 0.9, T 0.8, penalty 1.1, V 262144"}
         torch.cuda.empty_cache()

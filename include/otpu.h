@@ -153,14 +153,6 @@ int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8_t* da, int
                         int fmt, int flags, int k0, int64_t base, float* logits,
                         uint64_t* best, int32_t* token, otpu_stream_t stream);
 
-/* The same with the LM head's QACT in the launch (opentpu/llm/qwen3.py:2052-2088: QACT of the
- * normed hidden row, fp32.quantize_mx(x, 32), then the vocabulary MMs): x is the fp32 row [K],
- * quantized in each workgroup's prologue as otpu_mm_qin does.  K a multiple of 128 (int8) or
- * 256 (4-bit), at most 4096. */
-int otpu_lm_head_argmax_qin(const float* x, int K, const uint8_t* w, int64_t rs, const uint8_t* ws,
-                            int64_t srs, int N, int fmt, int flags, int k0, int64_t base,
-                            float* logits, uint64_t* best, int32_t* token, otpu_stream_t stream);
-
 /* VOP ARGMAX (opentpu/isasim.py:1141-1152, opentpu/isa.py:633): per row of x [rows, ldx] the
  * (maximum, i2f(first column + base)) fp32 pair into pairs[r * drs + 0..1]. */
 int otpu_argmax(const float* x, int rows, int cols, int64_t ldx, int64_t base, float* pairs,

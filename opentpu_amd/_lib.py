@@ -28,7 +28,6 @@ SIGNATURES = {
     "otpu_mm_batched": ([_I, _P, _L, _L, _P, _L, _P, _L, _L, _I, _I, _P, _L, _L, _P, _L, _L, _I, _I, _I,
                          _I, _P, _L, _L, _P], _I),
     "otpu_lm_head_argmax": ([_P, _P, _P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _L, _P, _P, _P, _P], _I),
-    "otpu_lm_head_argmax_qin": ([_P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _L, _P, _P, _P, _P], _I),
     "otpu_argmax": ([_P, _I, _I, _L, _L, _P, _L, _P], _I),
     "otpu_pack_int8": ([_P, _I, _I, _L, _I, _P, _L, _P, _L, _P], _I),
     "otpu_pack_x4": ([_P, _I, _I, _L, _I, _P, _L, _P, _L, _P], _I),

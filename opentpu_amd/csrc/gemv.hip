@@ -357,40 +357,6 @@ extern "C" int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8
     return otpu_launch_check("lm_head_argmax");
 }
 
-extern "C" int otpu_lm_head_argmax_qin(const float* x, int K, const uint8_t* w, int64_t rs, const uint8_t* ws,
-                                       int64_t srs, int N, int fmt, int flags, int k0, int64_t base, float* logits,
-                                       uint64_t* best, int32_t* token, otpu_stream_t stream) {
-    if (flags & (OTPU_ACC | OTPU_ASCALE | OTPU_RMAX))
-        return otpu_fail(OTPU_EINVAL, "lm_head_argmax_qin: no ACC, ASCALE or RMAX");
-    const int chunk = fmt == OTPU_INT8 ? OTPU_D : 2 * OTPU_D;
-    if (K < chunk || K % chunk || K > QIN_KMAX)
-        return otpu_fail(OTPU_EINVAL, "lm_head_argmax_qin: K %d (a multiple of %d, at most %d)", K, chunk, QIN_KMAX);
-    if (!x || !best || !token) return otpu_fail(OTPU_EINVAL, "lm_head_argmax_qin: NULL x, best or token");
-    if (!al(x, 16)) return otpu_fail(OTPU_EALIGN, "lm_head_argmax_qin: x 16-byte aligned");
-    if (!al(best, 8)) return otpu_fail(OTPU_EALIGN, "lm_head_argmax_qin: best 8-byte aligned");
-    if (base < 0 || base + (int64_t)N > 0xFFFFFFFFll)
-        return otpu_fail(OTPU_EINVAL, "lm_head_argmax_qin: base %lld", (long long)base);
-    int rc = check_mm("lm_head_argmax_qin", reinterpret_cast<const int8_t*>(x), K, reinterpret_cast<const uint8_t*>(x),
-                      K / 32, 1, K, w, rs, ws, srs, N, fmt, flags, k0);
-    if (rc) return rc;
-    hipStream_t s = (hipStream_t)stream;
-    MMArgs a = make_args(nullptr, K, nullptr, nullptr, K / 32, 1, K, w, rs, ws, srs, N, flags, k0);
-    a.out = logits; a.ors = N; a.best = best; a.base = base;
-    a.xin = x; a.xmul = nullptr; a.nsum = 1; a.sum_stride = K; a.xin_bs = K;
-    a.P = (fmt == OTPU_INT8 ? K : K / 2) / 16;
-    int L = 1;
-    pick_team(a.P, &a.T, &L);
-    fill_u32<<<1, 64, 0, s>>>(reinterpret_cast<uint32_t*>(best), 2, 0u);
-    switch (fmt) {
-        case OTPU_INT8: launch_qin_fmt<OTPU_INT8>(a, L, 1, s); break;
-        case OTPU_INT4: launch_qin_fmt<OTPU_INT4>(a, L, 1, s); break;
-        case OTPU_FP4: launch_qin_fmt<OTPU_FP4>(a, L, 1, s); break;
-        default: launch_qin_fmt<OTPU_NVFP4>(a, L, 1, s); break;
-    }
-    best_finish<<<1, 64, 0, s>>>(best, token);
-    return otpu_launch_check("lm_head_argmax_qin");
-}
-
 extern "C" int otpu_argmax(const float* x, int rows, int cols, int64_t ldx, int64_t base, float* pairs,
                            int64_t drs, otpu_stream_t stream) {
     if (rows < 1 || cols < 1 || ldx < cols || !x || !pairs || (rows > 1 && drs < 2))

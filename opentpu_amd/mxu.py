@@ -83,25 +83,6 @@ def lm_head_argmax(q, Sa, da, rows, srows, fmt: str, K: int, *, rsc: bool = Fals
     return tok, lg, best
 
 
-def lm_head_argmax_qin(x, rows, srows, fmt: str, *, rsc: bool = False, k0: int = 0, base: int = 0,
-                       logits: bool = True):
-    """The LM head from the fp32 hidden row x [K] (its QACT in the same launch,
-    `opentpu/llm/qwen3.py:2052-2088`): returns (token, logits or None, best) as lm_head_argmax."""
-    numpy_in = X.is_numpy(x)
-    xd = X.dev(np.ravel(x) if numpy_in else x.reshape(-1), np.float32)
-    wd, sd = X.dev(rows, np.uint8), X.dev(srows, np.uint8)
-    N, K = wd.shape[0], xd.shape[0]
-    lg = X.empty((N,), np.float32) if logits else None
-    best = X.empty((1,), np.int64)
-    tok = X.empty((1,), np.int32)
-    X.call("otpu_lm_head_argmax_qin", X.ptr(xd), K, X.ptr(wd), wd.shape[1], X.ptr(sd), sd.shape[1], N, X.FMT[fmt],
-           _flags(rsc=rsc), k0, base, X.ptr(lg), X.ptr(best), X.ptr(tok), X.stream())
-    if numpy_in:
-        return (int(X.host(tok)[0]), X.host(lg) if logits else None,
-                int(X.host(best).view(np.uint64)[0]))
-    return tok, lg, best
-
-
 def argmax(x, base: int = 0):
     """VOP ARGMAX of each row of x [rows, cols]: (max values [rows], first index + base [rows])
     (`opentpu/isasim.py:1141-1152`; the index comes back as the i2f'd fp32 the VOP writes)."""

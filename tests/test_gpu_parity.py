@@ -187,28 +187,6 @@ def test_lm_head_argmax_full_size(ops):
     assert same_bits(logits, want)
     t0, b0 = OC.argmax(want)
     assert tok == t0 == MM.greedy(want) and best == b0
-    say("lm head c5, QACT in the launch")
-    tok2, logits2, best2 = mxu.lm_head_argmax_qin(x, rows, srows, "int8", rsc=True)
-    assert same_bits(logits2, want) and tok2 == t0 and best2 == b0
-
-
-@pytest.mark.parametrize("fmt,K,N", [("int8", 1024, 5000), ("int4", 2048, 3000), ("fp4", 768, 777)])
-def test_lm_head_argmax_qin(ops, fmt, K, N):
-    """QACT of the fp32 hidden row in the LM head's launch: logits, token and best equal the
-    oracle's QACT, MM and argmax."""
-    _, _, mxu = ops
-    rng = np.random.default_rng(K + N)
-    W = (spread(rng, N, K, 1.5, 128) * 0.02).astype(np.float32)
-    rows, srows = (Q.pack_int8x(W) if fmt == "int8" else Q.pack_x4(W, fmt))
-    x = spread(rng, 1, K, 3.0, 32)
-    q, Sa, da = F.quantize_mx(x, 32)
-    say("lm head qin", fmt, K, N)
-    tok, logits, best = mxu.lm_head_argmax_qin(x, rows, srows, fmt, base=1000)
-    want = OC.mm(q, Sa, da, rows, srows, fmt, K)[0]
-    assert same_bits(logits, want)
-    t0, b0 = OC.argmax(want)                   # base 0: the index's complement in the low word
-    assert tok == 1000 + t0
-    assert best == ((b0 >> 32) << 32) | (~(1000 + t0) & 0xFFFFFFFF)
 
 
 def test_lm_head_ties_go_to_the_lowest_index(ops):
