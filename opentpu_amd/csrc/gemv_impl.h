@@ -482,7 +482,12 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a) {
         if (threadIdx.x == 0) {
             uint64_t m = red[0];
             for (int i = 1; i < (int)(blockDim.x >> 6); ++i) m = red[i] > m ? red[i] : m;
-            if (m) atomicMax(reinterpret_cast<unsigned long long*>(a.best), (unsigned long long)m);
+            // read the best word first and skip the atomic when it already holds more: the
+            // workgroups' atomics on one address serialize at the memory side, and once a large
+            // logit has landed most of them have nothing to add
+            auto* bp = reinterpret_cast<unsigned long long*>(a.best);
+            if (m && m > __hip_atomic_load(bp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                __hip_atomic_fetch_max(bp, (unsigned long long)m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
