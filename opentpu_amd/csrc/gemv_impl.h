@@ -513,12 +513,11 @@ __global__ __launch_bounds__(256) void gemv_qin_kernel(MMArgs a) {
 // or two row groups, so the last round of workgroups is short), 16 for four or more (the LM
 // head: the same from 16 to 64, 4% over 8), else 8; OTPU_GEMV_BLOCKS_PER_CU overrides
 inline int gemv_blocks_per_cu(int L) {
-    static int v = -1;
-    if (v < 0) {
+    static const int v = [] {                   // read once (thread-safe static initialisation)
         const char* e = getenv("OTPU_GEMV_BLOCKS_PER_CU");
-        int x = e ? atoi(e) : 0;
-        v = (x > 0 && x <= 64) ? x : 0;
-    }
+        const int x = e ? atoi(e) : 0;
+        return (x > 0 && x <= 64) ? x : 0;
+    }();
     return v ? v : (L == 1 ? 32 : (L >= 4 ? 16 : 8));
 }
 
