@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-Headline: the 4-bit group-32 decode GEMV, weights N=6144 x K=2048
+Headline (the metric's quoted configuration, c2): the 4-bit group-32 decode GEMV, weights N=6144 x K=2048
 int4x (opentpu/quant.py int4: nibbles + per-row Sw, per-block dw, per-32 multipliers m, from
 N(0, 0.02)), one int8 MX activation row from N(0, 1).  A step is one launch of B independent
 such GEMVs (B weight sets resident in HBM, > 512 MB in total, so no step is served from the
