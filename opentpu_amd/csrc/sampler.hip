@@ -18,9 +18,10 @@
 // of its groups (contiguous runs) ranked by their maxima the same way: a group outside those
 // has n groups above it, each holding an entry above every entry of it.  So A selects 16-block
 // groups (sbm) and then blocks among the chosen groups' blocks; B selects 16-candidate groups
-// and then candidates among theirs.  A selection of n among at most 1024 finds the n-th largest
-// key T by a 4-pass radix select (8 bits a pass), takes the keys above T and the first (by
-// position) keys equal to T, and orders them by a rank sort.  Knock-out can take a position
+// and then candidates among theirs.  The n chosen groups' maxima are n entries, so the second
+// step drops every entry below the least of them before it ranks.  A selection of n among at
+// most 1024 ranks each remaining entry by the number of remaining composites (key << 32 |
+// ~position, all distinct) above its own: rank r < n is knock-out slot r.  Knock-out can take a position
 // twice once everything left is -inf or below: the rounds past the m entries above -inf
 // (m >= 1) all take the first position among the taken ones and the -inf ones, with value
 // -inf; that is applied to the sorted list (only then is the first -inf position looked up).
@@ -136,11 +137,10 @@ __global__ __launch_bounds__(256) void sample_blocks(SampleArgs a) {
 }
 
 struct SelShared {
-    alignas(16) int hist[3][256];     // a pass's histogram; a pass clears the one two passes on
+    uint64_t cand[SRMAX * SNT];       // a selection's entries at or above its bound: key << 32 | ~position
     int wtot[SNT / 64];
     int first_ninf;
-    uint64_t comp[SKMAX];             // the n taken, unordered: key << 32 | ~position
-    uint32_t skey[SKMAX];             // ... in knock-out order
+    uint32_t skey[SKMAX];             // the n selected in knock-out order
     int spos[SKMAX];
 };
 
@@ -156,121 +156,57 @@ __device__ __forceinline__ int wave_scan(int v) {
     return v;
 }
 
-// histogram add with the lanes of a wave that share a bin folded into one atomic (the top
-// digits of nearby keys are few); after 4 folds the rest add one by one
-__device__ __forceinline__ void hist_add(int* H, bool on, int bin, int lane) {
-    uint64_t act = __ballot(on);
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        if (act) {
-            const int lead = __builtin_ctzll(act);
-            const int b = __builtin_amdgcn_readlane(bin, lead);
-            const uint64_t same = __ballot(on && bin == b) & act;
-            if (lane == lead) atomicAdd(&H[b], __popcll(same));
-            act &= ~same;
-        }
-    }
-    if ((act >> lane) & 1) atomicAdd(&H[bin], 1);
-}
-
-// The n (1 <= n <= min(64, count)) largest of count (<= 1024) entries: thread t holds the keys
-// of positions t R .. t R + R - 1 in kk (R = ceil(count / 256)) and their positions are pos(p).
-// Leaves in S.comp[0, n) the composites key << 32 | ~pos(p), unordered.  Every thread calls it.
+// The n (1 <= n <= min(64, count)) largest of count (<= 1024) entries by (key, then the lower
+// position), in that order, into S.skey / S.spos[0, n).  Thread t holds the keys of entries
+// t R .. t R + R - 1 in kk (R = ceil(count / 256)); pos(p) is entry p's position (distinct).
+// lo is a key that at least n entries reach (0: no bound), so no entry below it is among the
+// n.  The entries at or above lo are packed into S.cand; each one's rank is the number of
+// packed composites above its own, and the composites are distinct, so the ranks below n are
+// the n slots.  Every thread calls it.
 template <class PosFn>
-__device__ void select_set(int count, int n, const uint32_t (&kk)[SRMAX], int R, PosFn pos, SelShared& S) {
+__device__ void select_top(int count, int n, const uint32_t (&kk)[SRMAX], int R, uint32_t lo, PosFn pos,
+                           SelShared& S) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    S.hist[0][t] = 0;                                 // SNT == 256: one bin a thread
-    S.hist[1][t] = 0;
-    __syncthreads();
-    // radix select, 8 bits a pass: T = the n-th largest key (with multiplicity).  Every wave
-    // reads the histogram and finds the digit itself, so a pass has one barrier; the buffer a
-    // pass clears was last read two passes before, by waves that have since met a barrier.
-    uint32_t prefix = 0, maskhi = 0;
-    int remaining = n;
-    for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
-        int* H = S.hist[pass % 3];
+    int mine = 0;
 #pragma unroll
-        for (int r = 0; r < SRMAX; ++r) {
-            if (r < R) {                              // R is the same in every wave
-                const int p = t * R + r;
-                hist_add(H, p < count && (kk[r] & maskhi) == prefix, (kk[r] >> shift) & 255, lane);
-            }
-        }
-        if (pass < 3) S.hist[(pass + 1) % 3][t] = 0;
-        __syncthreads();
-        // lane l: bins 255-4l .. 252-4l (one 16-byte read), descending
-        const int4 hv = *reinterpret_cast<const int4*>(&H[252 - 4 * lane]);
-        const int c1 = hv.w, c2 = c1 + hv.z, c3 = c2 + hv.y, c4 = c3 + hv.x;
-        const int incl = wave_scan(c4);
-        const int before = incl - c4;
-        const bool mine = before < remaining && remaining <= incl;
-        const int need = remaining - before;          // in this lane's bins
-        const int j = need <= c1 ? 0 : (need <= c2 ? 1 : (need <= c3 ? 2 : 3));
-        const int dg = 255 - 4 * lane - j;
-        const int rm = need - (j == 0 ? 0 : (j == 1 ? c1 : (j == 2 ? c2 : c3)));
-        const int src = __builtin_ctzll(__ballot(mine));
-        prefix |= (uint32_t)__builtin_amdgcn_readlane(dg, src) << shift;
-        maskhi |= 0xFFu << shift;
-        remaining = __builtin_amdgcn_readlane(rm, src);
-    }
-    const uint32_t T = prefix;
-    const int c_gt = n - remaining;
-    // slots: the keys above T in any order, then the first `remaining` keys equal to T by
-    // position (positions grow with t R + r); one scan of both counts packed in 16-bit halves
-    int gtc = 0, eqc = 0;
-#pragma unroll
-    for (int r = 0; r < SRMAX; ++r) {
-        const int p = t * R + r;
-        const bool v = r < R && p < count;
-        gtc += (v && kk[r] > T) ? 1 : 0;
-        eqc += (v && kk[r] == T) ? 1 : 0;
-    }
-    const int both = gtc | (eqc << 16);
-    const int incl = wave_scan(both);
+    for (int r = 0; r < SRMAX; ++r) mine += (r < R && t * R + r < count && kk[r] >= lo) ? 1 : 0;
+    const int incl = wave_scan(mine);
     if (lane == 63) S.wtot[w] = incl;
+    if (t == 0) S.first_ninf = INT_MAX;
     __syncthreads();
-    int ex = incl - both;
-    for (int v = 0; v < w; ++v) ex += S.wtot[v];
-    int gslot = ex & 0xFFFF, erank = ex >> 16;
+    int off = incl - mine;
+    for (int v = 0; v < w; ++v) off += S.wtot[v];
+    const int c = S.wtot[0] + S.wtot[1] + S.wtot[2] + S.wtot[3];
 #pragma unroll
     for (int r = 0; r < SRMAX; ++r) {
         const int p = t * R + r;
-        if (!(r < R && p < count)) continue;
-        const uint64_t cp = ((uint64_t)kk[r] << 32) | (uint32_t)~(uint32_t)pos(p);
-        if (kk[r] > T) {
-            S.comp[gslot++] = cp;
-        } else if (kk[r] == T) {
-            if (erank < remaining) S.comp[c_gt + erank] = cp;
-            ++erank;
-        }
+        if (r < R && p < count && kk[r] >= lo) S.cand[off++] = ((uint64_t)kk[r] << 32) | (uint32_t)~(uint32_t)pos(p);
     }
     __syncthreads();
-}
-
-// S.comp[0, n) -> S.skey / S.spos in knock-out order.  ninf(): the first position holding
-// -inf in the whole list (INT_MAX if none), asked only when fewer than n entries are above
-// -inf.  Every thread calls it.
-template <class NinfFn>
-__device__ void knock_order(int n, NinfFn ninf, SelShared& S) {
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const uint64_t me = lane < n ? S.comp[lane] : 0;
-    const uint32_t mk = (uint32_t)(me >> 32);
-    int m = __popcll(__ballot(lane < n && mk > KEY_NINF));     // the same in every wave
-    m = m < 1 ? 1 : m;
-    if (w == 0) {
-        int rk = 0;                                   // distinct composites
-#pragma unroll
-        for (int j = 0; j < SKMAX; ++j) rk += (j < n && S.comp[j] > me) ? 1 : 0;
-        if (lane < n) {
-            S.skey[rk] = mk;
+    for (int i = t; i < c; i += SNT) {
+        const uint64_t me = S.cand[i];
+        int rk = 0;
+#pragma unroll 8
+        for (int j = 0; j < c; ++j) rk += S.cand[j] > me ? 1 : 0;
+        if (rk < n) {
+            S.skey[rk] = (uint32_t)(me >> 32);
             S.spos[rk] = (int)~(uint32_t)me;
         }
-        if (lane == 0) S.first_ninf = INT_MAX;
     }
     __syncthreads();
+}
+
+// The knock-out rule's corner on S.skey / S.spos[0, n) (knock-out order): the rounds past the
+// m entries above -inf (m >= 1) take, with value -inf, the first position among the m taken
+// ones and the -inf ones.  ninf(): a per-thread part of the first position holding -inf in the
+// whole list (INT_MAX if none), asked only when m < n.  Every thread calls it.
+template <class NinfFn>
+__device__ void ninf_corner(int n, NinfFn ninf, SelShared& S) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    int m = __popcll(__ballot(lane < n && S.skey[lane] > KEY_NINF));   // the same in every wave
+    m = m < 1 ? 1 : m;
     if (m < n) {                                      // uniform
-        int fm = ninf();                              // a per-thread partial
+        int fm = ninf();
         for (int o = 32; o > 0; o >>= 1) fm = min(fm, __shfl_xor(fm, o, 64));
         if (lane == 0 && fm != INT_MAX) atomicMin(&S.first_ninf, fm);
         __syncthreads();
@@ -286,20 +222,6 @@ __device__ void knock_order(int n, NinfFn ninf, SelShared& S) {
         }
         __syncthreads();
     }
-}
-
-// wave 0: the positions of S.comp[0, g) into v[0, g) in ascending order (the chosen groups,
-// so that the next selection's positions ascend with its entry numbers); then a barrier
-__device__ __forceinline__ void groups_sorted(int* v, int g, const SelShared& S) {
-    const int t = threadIdx.x;
-    if (t < 64) {
-        const int me = t < g ? (int)~(uint32_t)S.comp[t] : INT_MAX;
-        int rk = 0;
-#pragma unroll
-        for (int j = 0; j < SKMAX; ++j) rk += (j < g && (int)~(uint32_t)S.comp[j] < me) ? 1 : 0;
-        if (t < g) v[rk] = me;
-    }
-    __syncthreads();
 }
 
 // the 64-partial folding tree over x[0 .. 63] (partial c = +0 + x[c]): first half plus second
@@ -322,8 +244,10 @@ __global__ __launch_bounds__(SNT) void sample_pick(SampleArgs a) {
     const int nb = a.nb, nsb = (nb + SGRP - 1) / SGRP;
     const int nA = a.k < nb ? a.k : nb;
     uint32_t kk[SRMAX];
-    // A1: the nA largest groups of 16 blocks (by sbm), as a set
+    // A1: the nA largest groups of 16 blocks (by sbm); loA: the least of their maxima when they
+    // are nA groups (each holds a block at or above it), else 0
     const int gA = nA < nsb ? nA : nsb;
+    uint32_t loA = 0u;
     {
         const int R = (nsb + SNT - 1) / SNT;
 #pragma unroll
@@ -332,12 +256,13 @@ __global__ __launch_bounds__(SNT) void sample_pick(SampleArgs a) {
             kk[r] = (r < R && p < nsb) ? fkey_f(a.sbm[p]) : 0u;
         }
         if (gA < nsb) {
-            select_set(nsb, gA, kk, R, [](int p) { return p; }, S);
-            groups_sorted(grp, gA, S);
-        } else {
-            if (t < gA) grp[t] = t;
-            __syncthreads();
+            select_top(nsb, gA, kk, R, 0u, [](int p) { return p; }, S);
+            if (t < gA) grp[t] = S.spos[t];
+            loA = S.skey[gA - 1];
+        } else if (t < gA) {
+            grp[t] = t;
         }
+        __syncthreads();
     }
     // A2: the nA largest blocks among the chosen groups' (positions: block ids), in order
     {
@@ -348,9 +273,9 @@ __global__ __launch_bounds__(SNT) void sample_pick(SampleArgs a) {
             const int b = (r < R && p < cnt) ? grp[p >> 4] * SGRP + (p & 15) : nb;
             kk[r] = b < nb ? fkey_f(a.bm[b]) : 0u;        // blocks past nb: below every key
         }
-        select_set(cnt, nA, kk, R, [](int p) { return grp[p >> 4] * SGRP + (p & 15); }, S);
+        select_top(cnt, nA, kk, R, loA, [](int p) { return grp[p >> 4] * SGRP + (p & 15); }, S);
         const float* bm = a.bm;
-        knock_order(nA, [bm, nb, t]() {
+        ninf_corner(nA, [bm, nb, t]() {
             int f = INT_MAX;
             for (int b = t; b < nb; b += SNT)
                 if (fkey_f(bm[b]) == KEY_NINF) f = min(f, b);
@@ -360,8 +285,9 @@ __global__ __launch_bounds__(SNT) void sample_pick(SampleArgs a) {
         __syncthreads();
     }
     // B1: the k largest groups of 16 candidates (candidate c: block qA[c / 64]'s logit c % 64;
-    // -inf past nA blocks), by their maxima, as a set
+    // -inf past nA blocks), by their maxima; loB: the least of those maxima
     const float* lg = a.lg;
+    uint32_t loB;
     const int nc = a.km * SBLK, ngc = nc / SGRP;
     {
         // thread t: group t's maximum (ngc <= 256)
@@ -379,8 +305,10 @@ __global__ __launch_bounds__(SNT) void sample_pick(SampleArgs a) {
             }
         }
         kk[0] = g;
-        select_set(ngc, a.k, kk, 1, [](int p) { return p; }, S);
-        groups_sorted(grp, a.k, S);
+        select_top(ngc, a.k, kk, 1, 0u, [](int p) { return p; }, S);
+        if (t < a.k) grp[t] = S.spos[t];
+        loB = S.skey[a.k - 1];
+        __syncthreads();
     }
     // B2: the k largest candidates among the chosen groups' (positions: candidate numbers)
     {
@@ -395,8 +323,8 @@ __global__ __launch_bounds__(SNT) void sample_pick(SampleArgs a) {
             }
             kk[r] = key;
         }
-        select_set(cnt, a.k, kk, R, [](int p) { return grp[p >> 4] * SGRP + (p & 15); }, S);
-        knock_order(a.k, [lg, nc, nA, t]() {
+        select_top(cnt, a.k, kk, R, loB, [](int p) { return grp[p >> 4] * SGRP + (p & 15); }, S);
+        ninf_corner(a.k, [lg, nc, nA, t]() {
             int f = INT_MAX;
             for (int c = t; c < nc; c += SNT) {
                 const int j = c >> 6;

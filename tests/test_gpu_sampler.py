@@ -70,6 +70,30 @@ def test_candidates_and_picks_match_the_oracle(S, V, T, k, P, R, cap, masked):
     assert np.array_equal(ids.cpu().numpy(), SP.pick(lg, osamp, ctx, u, cap or None))
 
 
+@pytest.mark.parametrize("V,grid,k", [(262144, 1.0, 50), (262144, 0.0, 64), (5000, 0.5, 64), (70000, 2.0, 33)])
+def test_heavy_ties_match_the_oracle(S, V, grid, k):
+    """Logits on a coarse grid (grid 0: every logit equal), so that many blocks share the
+    largest maxima and many candidates sit exactly at a selection's bound: the order among
+    equal keys comes from the positions alone."""
+    say(f"sampler heavy ties V={V} grid={grid} k={k}")
+    rng = np.random.default_rng(V + k + 7)
+    if grid:
+        lg = (np.round(rng.standard_normal(V) * 3 / grid) * grid).astype(np.float32)
+    else:
+        lg = np.full(V, 1.5, np.float32)
+    ctx = rng.integers(0, V, 30).tolist()
+    samp, osamp = S.Sampling(1.0, k, 0.9, 1.1), SP.Sampling(1.0, k, 0.9, 1.1)
+    u = ((np.arange(300) + 0.5) / 300).astype(np.float32)
+    import torch
+    sm = S.Sampler(V, samp, ctx)
+    ids = sm.pick_device(torch.from_numpy(lg).cuda(), torch.from_numpy(u).cuda())
+    sm.check()
+    vs, si = sm.candidates()
+    vs0, si0 = SP.candidates(lg, osamp, ctx, None)
+    assert same_bits(vs, vs0) and np.array_equal(si, si0)
+    assert np.array_equal(ids.cpu().numpy(), SP.pick(lg, osamp, ctx, u, None))
+
+
 def test_lm_head_then_sample(S):
     """An int8 LM head (vocabulary 65536 x 1024) and the sampler on one stream: the ids are the
     oracle's pick over the oracle MM's logits."""
