@@ -36,6 +36,7 @@ constexpr int SKMAX = 64;                 // the largest top-k
 constexpr int SNT = 256;                  // sample_pick's threads
 constexpr int SRMAX = 4;                  // entries a thread in a selection (at most 1024)
 constexpr int SGRP = 16;                  // a selection group: 16 blocks, or 16 candidates
+constexpr int SRB = 16;                   // candidates a thread in B's direct selection (4096 / 256)
 constexpr int NB_MAX = SRMAX * SNT * SGRP;   // blocks (16384: a vocabulary of 1M)
 constexpr uint32_t KEY_NINF = 0x007FFFFFu;   // fkey(-inf)
 
@@ -156,20 +157,21 @@ __device__ __forceinline__ int wave_scan(int v) {
     return v;
 }
 
-// The n (1 <= n <= min(64, count)) largest of count (<= 1024) entries by (key, then the lower
+// The n (1 <= n <= min(64, count)) largest of count (<= 256 RM) entries by (key, then the lower
 // position), in that order, into S.skey / S.spos[0, n).  Thread t holds the keys of entries
-// t R .. t R + R - 1 in kk (R = ceil(count / 256)); pos(p) is entry p's position (distinct).
-// lo is a key that at least n entries reach (0: no bound), so no entry below it is among the
-// n.  The entries at or above lo are packed into S.cand; each one's rank is the number of
-// packed composites above its own, and the composites are distinct, so the ranks below n are
-// the n slots.  Every thread calls it.
-template <class PosFn>
-__device__ void select_top(int count, int n, const uint32_t (&kk)[SRMAX], int R, uint32_t lo, PosFn pos,
+// t R .. t R + R - 1 in kk (R = ceil(count / 256) <= RM); pos(p) is entry p's position
+// (distinct).  lo is a key that at least n entries reach (0: no bound), so no entry below it is
+// among the n.  The entries at or above lo are packed into S.cand; each one's rank is the number
+// of packed composites above its own, and the composites are distinct, so the ranks below n are
+// the n slots.  Returns false, having written nothing, when more than 1024 entries reach lo
+// (never for count <= 1024).  Every thread calls it.
+template <int RM, class PosFn>
+__device__ bool select_top(int count, int n, const uint32_t (&kk)[RM], int R, uint32_t lo, PosFn pos,
                            SelShared& S) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     int mine = 0;
 #pragma unroll
-    for (int r = 0; r < SRMAX; ++r) mine += (r < R && t * R + r < count && kk[r] >= lo) ? 1 : 0;
+    for (int r = 0; r < RM; ++r) mine += (r < R && t * R + r < count && kk[r] >= lo) ? 1 : 0;
     const int incl = wave_scan(mine);
     if (lane == 63) S.wtot[w] = incl;
     if (t == 0) S.first_ninf = INT_MAX;
@@ -177,8 +179,12 @@ __device__ void select_top(int count, int n, const uint32_t (&kk)[SRMAX], int R,
     int off = incl - mine;
     for (int v = 0; v < w; ++v) off += S.wtot[v];
     const int c = S.wtot[0] + S.wtot[1] + S.wtot[2] + S.wtot[3];
+    if (c > SRMAX * SNT) {                            // uniform; S.wtot is free again past the barrier
+        __syncthreads();
+        return false;
+    }
 #pragma unroll
-    for (int r = 0; r < SRMAX; ++r) {
+    for (int r = 0; r < RM; ++r) {
         const int p = t * R + r;
         if (r < R && p < count && kk[r] >= lo) S.cand[off++] = ((uint64_t)kk[r] << 32) | (uint32_t)~(uint32_t)pos(p);
     }
@@ -194,6 +200,7 @@ __device__ void select_top(int count, int n, const uint32_t (&kk)[SRMAX], int R,
         }
     }
     __syncthreads();
+    return true;
 }
 
 // The knock-out rule's corner on S.skey / S.spos[0, n) (knock-out order): the rounds past the
@@ -284,55 +291,80 @@ __global__ __launch_bounds__(SNT) void sample_pick(SampleArgs a) {
         if (t < nA) qA[t] = S.spos[t];
         __syncthreads();
     }
-    // B1: the k largest groups of 16 candidates (candidate c: block qA[c / 64]'s logit c % 64;
-    // -inf past nA blocks), by their maxima; loB: the least of those maxima
+    // B: the k largest of the km x 64 candidates (candidate c: block qA[c / 64]'s logit c % 64;
+    // -inf past nA blocks).  B0, directly: when A took k blocks, their maxima are k candidates,
+    // so none below the least of them is among the k.  When ties leave more than 1024 candidates
+    // at or above it, B1 and B2 select groups of 16 candidates first.
     const float* lg = a.lg;
-    uint32_t loB;
     const int nc = a.km * SBLK, ngc = nc / SGRP;
+    bool done;
     {
-        // thread t: group t's maximum (ngc <= 256)
-        uint32_t g = 0u;
-        if (t < ngc) {
-            const int j = t >> 2;
-            g = KEY_NINF;
-            if (j < nA) {
-                const float4* src = reinterpret_cast<const float4*>(lg + qA[j] * SBLK + 16 * (t & 3));
+        const uint32_t lo = nA == a.k ? S.skey[nA - 1] : 0u;
+        const int R = nc / SNT;                       // 2 .. 16, even (km is a multiple of 8)
+        uint32_t kb[SRB];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 v = src[q];
-                    g = max(g, max(max(fkey_f(v.x), fkey_f(v.y)), max(fkey_f(v.z), fkey_f(v.w))));
+        for (int r = 0; r < SRB; r += 2) {
+            // candidates c, c + 1 (c even) share a block; a thread's run may span two blocks
+            const int c = t * R + r, j = c >> 6;
+            uint32_t k0 = KEY_NINF, k1 = KEY_NINF;
+            if (r < R && j < nA) {
+                const float2 v = *reinterpret_cast<const float2*>(lg + qA[j] * SBLK + (c & 63));
+                k0 = fkey_f(v.x);
+                k1 = fkey_f(v.y);
+            }
+            kb[r] = k0;
+            kb[r + 1] = k1;
+        }
+        done = select_top(nc, a.k, kb, R, lo, [](int p) { return p; }, S);
+    }
+    if (!done) {
+        // B1: the k largest groups of 16 candidates by their maxima; loB: the least of those
+        uint32_t loB;
+        {
+            // thread t: group t's maximum (ngc <= 256)
+            uint32_t g = 0u;
+            if (t < ngc) {
+                const int j = t >> 2;
+                g = KEY_NINF;
+                if (j < nA) {
+                    const float4* src = reinterpret_cast<const float4*>(lg + qA[j] * SBLK + 16 * (t & 3));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 v = src[q];
+                        g = max(g, max(max(fkey_f(v.x), fkey_f(v.y)), max(fkey_f(v.z), fkey_f(v.w))));
+                    }
                 }
             }
+            kk[0] = g;
+            select_top(ngc, a.k, kk, 1, 0u, [](int p) { return p; }, S);
+            if (t < a.k) grp[t] = S.spos[t];
+            loB = S.skey[a.k - 1];
+            __syncthreads();
         }
-        kk[0] = g;
-        select_top(ngc, a.k, kk, 1, 0u, [](int p) { return p; }, S);
-        if (t < a.k) grp[t] = S.spos[t];
-        loB = S.skey[a.k - 1];
-        __syncthreads();
-    }
-    // B2: the k largest candidates among the chosen groups' (positions: candidate numbers)
-    {
-        const int cnt = a.k * SGRP, R = (cnt + SNT - 1) / SNT;
+        // B2: the k largest candidates among the chosen groups' (positions: candidate numbers)
+        {
+            const int cnt = a.k * SGRP, R = (cnt + SNT - 1) / SNT;
 #pragma unroll
-        for (int r = 0; r < SRMAX; ++r) {
-            const int p = t * R + r;
-            uint32_t key = 0u;
-            if (r < R && p < cnt) {
-                const int c = grp[p >> 4] * SGRP + (p & 15), j = c >> 6;
-                key = j < nA ? fkey_f(lg[qA[j] * SBLK + (c & 63)]) : KEY_NINF;
+            for (int r = 0; r < SRMAX; ++r) {
+                const int p = t * R + r;
+                uint32_t key = 0u;
+                if (r < R && p < cnt) {
+                    const int c = grp[p >> 4] * SGRP + (p & 15), j = c >> 6;
+                    key = j < nA ? fkey_f(lg[qA[j] * SBLK + (c & 63)]) : KEY_NINF;
+                }
+                kk[r] = key;
             }
-            kk[r] = key;
+            select_top(cnt, a.k, kk, R, loB, [](int p) { return grp[p >> 4] * SGRP + (p & 15); }, S);
         }
-        select_top(cnt, a.k, kk, R, loB, [](int p) { return grp[p >> 4] * SGRP + (p & 15); }, S);
-        ninf_corner(a.k, [lg, nc, nA, t]() {
-            int f = INT_MAX;
-            for (int c = t; c < nc; c += SNT) {
-                const int j = c >> 6;
-                if (j >= nA || fkey_f(lg[qA[j] * SBLK + (c & 63)]) == KEY_NINF) f = min(f, c);
-            }
-            return f;
-        }, S);
     }
+    ninf_corner(a.k, [lg, nc, nA, t]() {
+        int f = INT_MAX;
+        for (int c = t; c < nc; c += SNT) {
+            const int j = c >> 6;
+            if (j >= nA || fkey_f(lg[qA[j] * SBLK + (c & 63)]) == KEY_NINF) f = min(f, c);
+        }
+        return f;
+    }, S);
     if (w != 0) return;
     // C: one wave
     const int km = a.km;
