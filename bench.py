@@ -109,7 +109,7 @@ def batched_gemv(fmt, B, N, K, seed, steps, warmup, rsc=False):
         X.call("otpu_mm_batched", B, X.ptr(q), K, K, X.ptr(Sa), 1, X.ptr(da), K // 32, K // 32, 1, K,
                X.ptr(rows), rs, N * rs, X.ptr(srows), srs, N * srs, N, X.FMT[fmt], fl, 0, X.ptr(out), N, N, X.stream())
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
-    return ms, (rows, srows, q, Sa, da)
+    return ms, (rows, srows, q, Sa, da, out)
 
 
 def single_gemv_ms(fmt, batch, N, K, steps, rsc=False):
@@ -118,7 +118,7 @@ def single_gemv_ms(fmt, batch, N, K, steps, rsc=False):
     import torch
 
     from opentpu_amd import _lib as X
-    rows, srows, q, Sa, da = batch
+    rows, srows, q, Sa, da = batch[:5]
     B = rows.shape[0]
     out = torch.empty((1, N), dtype=torch.float32, device="cuda")
     it = [0]
@@ -144,7 +144,7 @@ def lm_head(steps, warmup):
     x = torch.randn((1, K), generator=gen, device="cuda")
     q, Sa, da = fp32.quantize_mx(x, 32)
     logits = torch.empty((N,), dtype=torch.float32, device="cuda")
-    best = torch.empty((1,), dtype=torch.int64, device="cuda")
+    best = torch.zeros((2,), dtype=torch.int64, device="cuda")      # result word, running maximum
     tok = torch.empty((1,), dtype=torch.int32, device="cuda")
 
     def step():
@@ -276,23 +276,35 @@ def summarize(outdir):
             print(f"{n:10d}  {key[1]:>10}  {means}  {key[0]}")
 
 
-def cpu_baseline(seconds=10.0):
-    """The C oracle (OpenMP) on this host: one c2 GEMV repeated for about `seconds` on
-    min(16, cores) threads; beside it (in `also`) the same C code on one thread and the numpy
-    oracle (float64 group sums, the reference simulator's method), each on a few calls."""
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(sample, seconds=10.0):
+    """The C oracle (OpenMP) on this host, on the timed workload's first problem (its weights,
+    activation row and the GPU's output copied back from the device): one c2 GEMV repeated for
+    about `seconds` on min(16, cores) threads, its output checked against the GPU's bit for
+    bit; beside it (in `also`) the same C code on one thread and the numpy oracle (float64
+    group sums, the reference simulator's method), each on a few calls."""
     from oracle import cpu as OC
-    from oracle import formats as Q
-    from oracle import fp32 as F
+    from oracle import mm as MM
     threads = min(16, os.cpu_count() or 1)
     OC.threads(threads)
-    rng = np.random.default_rng(2)
     N, K = 6144, 2048
-    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
-    rows, srows = Q.pack_x4(W, "int4")
-    q, Sa, da = F.quantize_mx(rng.standard_normal((1, K)).astype(np.float32), 32)
+    rows, srows, q, Sa, da, gpu_out = (t.cpu().numpy() for t in sample)
+    q, Sa, da, gpu_out = q[:1], Sa[:1], da[:1], gpu_out[:1]
     t0 = time.perf_counter()
-    OC.mm(q, Sa, da, rows, srows, "int4", K)
+    want = OC.mm(q, Sa, da, rows, srows, "int4", K)
     one = time.perf_counter() - t0
+    matches = bool(np.array_equal(want.view(np.uint32), gpu_out.view(np.uint32)))
     reps = max(1, min(2000, int(seconds / max(one, 1e-4))))
     t0 = time.perf_counter()
     for _ in range(reps):
@@ -304,14 +316,14 @@ def cpu_baseline(seconds=10.0):
         OC.mm(q, Sa, da, rows, srows, "int4", K)
     dt1 = (time.perf_counter() - t0) / 20
     OC.threads(threads)
-    from oracle import mm as MM
     t0 = time.perf_counter()
     for _ in range(3):
         MM.mm(q, Sa, da, rows, srows, "int4", K)
     dtn = (time.perf_counter() - t0) / 3
     return {"value": round(c2_bytes() / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"c2 int4 GEMV 6144x2048, {reps} calls of the C oracle (oracle/cpu_mm.c, OpenMP), "
-                      f"{dt * 1e3:.2f} ms per call",
+            "sample": f"c2 int4 GEMV 6144x2048 (problem 0 of the timed launch), {reps} calls of the C oracle "
+                      f"(oracle/cpu_mm.c, OpenMP), {dt * 1e3:.2f} ms per call",
+            "cpu_model": cpu_model(), "gpu_output_matches": matches,
             "also": {"c_1_thread_GBps": round(c2_bytes() / dt1 / 1e9, 3), "c_1_thread_ms": round(dt1 * 1e3, 2),
                      "numpy_oracle_GBps": round(c2_bytes() / dtn / 1e9, 3), "numpy_oracle_ms": round(dtn * 1e3, 1),
                      "host_cores": os.cpu_count()}}
@@ -347,11 +359,14 @@ def main():
     ms2, single2 = batched_gemv("int4", B2, N2, K2, 2, args.steps, args.warmup)
     gbs2 = B2 * c2_bytes() / (ms2 * 1e-3) / 1e9
     print(f"[c2] batched int4 GEMV: {ms2:.4f} ms/step, {gbs2:.1f} GB/s", file=sys.stderr, flush=True)
+    rows2, srows2, q2, Sa2, da2, out2 = single2
+    sample2 = (rows2[0], srows2[0], q2[:1], Sa2[:1], da2[:1], out2[:1].clone())
     if "c2s" in only:
         ms2s = single_gemv_ms("int4", single2, N2, K2, 200)
         extra["c2_single_launch"] = {"us": round(ms2s * 1e3, 3),
                                      "GBps": round(c2_bytes() / (ms2s * 1e-3) / 1e9, 1)}
-    del single2
+    sample2 = tuple(t.cpu() for t in sample2)
+    del single2, rows2, srows2, q2, Sa2, da2, out2
     torch.cuda.empty_cache()
 
     if "copy" in only:
@@ -397,7 +412,7 @@ def main():
                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         print(f"[c3 mx] {extra['c3_gemm_mx_x_rsc']}", file=sys.stderr, flush=True)
 
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None if args.no_cpu else cpu_baseline(sample2)
     line = {
         "metric": "quant GEMV GB/s (% HBM peak) + prefill int8 GEMM TOPS, 1 MI355X",
         "value": round(gbs2, 2),
@@ -409,7 +424,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": "int4 weights x int8 activations (int32 dot, exact int64 accumulate, fp32 epilogue)",
         "data": "synthetic (seeded N(0,0.02) weights packed on the GPU, N(0,1) activations)",
         "config": {"workload": f"c2: 4-bit int4x group-32 decode GEMV N={N2} K={K2}, {B2} independent "
                                f"weight sets per launch", "batch": B2, "N": N2, "K": K2, "fmt": "int4"},

@@ -47,25 +47,53 @@ enum {
     OTPU_RSC = 0x80
 };
 
+/* QACT / QST flags (the reference's QACT bits: opentpu/isa.py, docs/isa.md:444-460).  CSCALE,
+ * RSCALE and ST are given by their operands (non-NULL cscale, rscale, qrows); DUP (the operand
+ * layout of MM PAIR) changes no result and has no counterpart. */
+enum {
+    OTPU_Q_ROW = 0x1,   /* one scale a row: every group offset 0 */
+    OTPU_Q_LO = 0x10,   /* the split's lo part: q8lo bytes and the scale S * 2^-8 (SPLITQ) */
+    OTPU_Q_HL = 0x20    /* both parts from one read: hi bytes at q[r, 0..K), lo at q[r, K..2K) */
+};
+#define OTPU_QALIGN 64  /* QACT ST / LDA rows: addresses and stride multiples of it (isa.py:40) */
+
 const char* otpu_last_error(void);
 int otpu_version(void);
 
-/* QACT's quantizer: fp32.quantize_mx(x, g, row_mode) of M rows of K
- * (opentpu/fp32.py:321-343; the instruction: opentpu/isasim.py:913-959, opentpu/isa.py:551).
+/* QACT: fp32.quantize_mx(x', g, row_mode, lo) of M rows of K (opentpu/fp32.py:321-343; the
+ * instruction: opentpu/isasim.py:913-959, opentpu/isa.py:551, docs/isa.md:444-486), x' the rows
+ * after QACT's pre-multiplies: x' = (x * rscale[r]) * cscale[c] (RSCALE, CSCALE; either may be
+ * NULL: RMSNorm's x * r * gamma folded into the quantizer).
  *   x [M, ldx] fp32 -> q [M, ldq] int8, S [M] fp32 (amax * f32(1/127)), d [M, ldd] uint8
- *   (K/g power-of-two group offsets; all 0 with row_mode).  g in {8, 16, 32, 64, 128}
- *   (QACT: 32 = D/4; QST and the int8x weight packer: 128 = D), K a multiple of g and of 4. */
-int otpu_qact(const float* x, int M, int K, int64_t ldx, int g, int row_mode, int8_t* q,
-              int64_t ldq, float* S, uint8_t* d, int64_t ldd, otpu_stream_t stream);
+ *   (K/g power-of-two group offsets; all 0 with OTPU_Q_ROW).  g in {8, 16, 32, 64, 128}
+ *   (QACT: 32 = D/4; QST and the int8x weight packer: 128 = D), K a multiple of g and of 4.
+ *   OTPU_Q_LO: q holds q8lo's bytes and S the scale S * 2^-8 (fp32.q8lo, opentpu/fp32.py:175-185).
+ *   OTPU_Q_HL: ldq >= 2K; q[r, 0..K) the hi bytes, q[r, K..2K) the lo bytes; S [2M]: S[r] hi's,
+ *   S[M + r] lo's; the same offsets d.
+ *   qrows (may be NULL; not with HL): QACT ST's rows, row r at qrows + r * qrs bytes: its K bytes
+ *   as q holds them, then block k's 8-byte record at K + 8k (S little-endian, the block's 4
+ *   offsets); g 32, K a multiple of 128 (at most 256 blocks), qrows and qrs (with M > 1)
+ *   multiples of OTPU_QALIGN, qrs >= K + 8 K/128 (opentpu/isasim.py:962-988, isa.py:577-580). */
+int otpu_qact(const float* x, int M, int K, int64_t ldx, int g, int flags, const float* rscale,
+              const float* cscale, int8_t* q, int64_t ldq, float* S, uint8_t* d, int64_t ldd,
+              uint8_t* qrows, int64_t qrs, otpu_stream_t stream);
+
+/* LDA (opentpu/isasim.py:990-1006): QACT ST's rows of KB blocks back into an MM operand:
+ * q [rows, ldq] the bytes, d [rows, ldd] the offsets (4 a block), S [KB, rows] (block k's record
+ * scale of row r at S[k * rows + r]: the MM over blocks from k on takes Sa = S + k * rows). */
+int otpu_lda(const uint8_t* qrows, int64_t qrs, int rows, int KB, int8_t* q, int64_t ldq, float* S,
+             uint8_t* d, int64_t ldd, otpu_stream_t stream);
 
 /* QACT over K / width equal column ranges of each row in one launch: one QACT instruction per
  * range (opentpu/isasim.py:927-959), as the reference quantizes a down projection's input in
  * F-chunks (opentpu/kernels/mlp.py:8-30, :87-120).  Range r of row j: q[j, r*width ..], its
  * scale S[r * M + j], its offsets d[j, r*width/g ..].  xmul (may be NULL): quantize the VOP MUL
- * x * xmul instead of x (same shape and stride; the SwiGLU product g * u of mlp.py:101-104). */
+ * x * xmul instead of x (same shape and stride; the SwiGLU product g * u of mlp.py:101-104);
+ * then RSCALE / CSCALE as otpu_qact (cscale indexed by the row's column, over all ranges).
+ * flags: OTPU_Q_ROW, OTPU_Q_LO. */
 int otpu_qact_ranges(const float* x, const float* xmul, int M, int K, int64_t ldx, int width, int g,
-                     int row_mode, int8_t* q, int64_t ldq, float* S, uint8_t* d, int64_t ldd,
-                     otpu_stream_t stream);
+                     int flags, const float* rscale, const float* cscale, int8_t* q, int64_t ldq,
+                     float* S, uint8_t* d, int64_t ldd, otpu_stream_t stream);
 
 /* VOP MUL (opentpu/isasim.py:1181, V_MUL; fp32.mul, opentpu/fp32.py:100): out = a * b, one IEEE RNE
  * product with flush-to-zero on operands and result, over n elements. */
@@ -110,23 +138,40 @@ int otpu_mm_ranges(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t*
  * otpu_qact_ranges + otpu_mm_ranges do without their ACC fold: range r writes its MM output
  * row to out + r * part_stride (one range: out).  The row quantized is x[0..K) folded with
  * nsum - 1 more rows sum_stride apart in order (x_0 + x_1 + ..: the ACC chain of a previous
- * per-range MM, opentpu/isasim.py:899-905), times xmul when given (VOP MUL).  No ACC / ASCALE /
- * RMAX; width at most 4096, a multiple of 128 (int8) or 256 (4-bit); nsum at most 16. */
-int otpu_mm_qin(const float* x, const float* xmul, int nsum, int64_t sum_stride, int K, int width,
-                const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
-                int k0, float* out, int64_t ors, int64_t part_stride, otpu_stream_t stream);
+ * per-range MM, opentpu/isasim.py:899-905), times xmul when given (VOP MUL), then QACT's
+ * RSCALE and CSCALE products (x * rscale[0]) * cscale[c] when given (rscale: one float, the
+ * row's factor; cscale [K]; docs/isa.md:447-452).  No ACC / ASCALE / RMAX; width at most 4096,
+ * a multiple of 128 (int8) or 256 (4-bit); nsum at most 16. */
+int otpu_mm_qin(const float* x, const float* xmul, const float* rscale, const float* cscale, int nsum,
+                int64_t sum_stride, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
+                int64_t srs, int N, int fmt, int flags, int k0, float* out, int64_t ors, int64_t part_stride,
+                otpu_stream_t stream);
 
 /* The chained layer's down projection folded in one launch (Builder.dot's per-range MMs with
  * their ACC, opentpu/compiler.py:2686-2720; swiglu_down's chunk loop,
- * opentpu/kernels/mlp.py:87-120): the fp32 row mul(x, xmul) (xmul may be NULL) in K / 256
- * ranges of 256 columns (the 4-bit down chunk at F = 3072, opentpu/kernels/mlp.py:8-24), each
+ * opentpu/kernels/mlp.py:87-120): the fp32 row mul(x, xmul) (xmul may be NULL; then RSCALE and
+ * CSCALE as otpu_mm_qin, either may be NULL) in K / 256 ranges of 256 columns (the 4-bit down chunk at F = 3072, opentpu/kernels/mlp.py:8-24), each
  * quantized by its own QACT and multiplied by its weight columns, and the ranges' outputs added
  * in range order into out[0..N): otpu_mm_qin's ranges and the fold of their rows, bit for bit.
  * 4-bit weights with scale rows only (INT4, FP4, NVFP4; no flags but PAIR); K a multiple of 256,
  * at most 4096. */
-int otpu_mm_qin_fold(const float* x, const float* xmul, int K, const uint8_t* w, int64_t rs,
-                     const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0, float* out,
-                     otpu_stream_t stream);
+int otpu_mm_qin_fold(const float* x, const float* xmul, const float* rscale, const float* cscale, int K,
+                     const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
+                     int k0, float* out, otpu_stream_t stream);
+
+/* MM SPL (split terms: opentpu/isasim.py:757-770, :849-852, :872-873; docs/isa.md:414-441): one
+ * MM over a split operand's terms, one K-block (128) of int8 RSC weights a part, natural rows.
+ *   q [M, ldq]: the activations' hi part at q[j, 0..128), with nterms 3 also the lo part at
+ *   q[j, 128..256) (otpu_qact OTPU_Q_HL's layout); Sa [M] and da [M, ldda] (4 offsets) the hi
+ *   part's; w: N hi weight rows rs bytes apart, their lo rows hld bytes after them (otpu_pack_int8
+ *   with OTPU_Q_ROW, then OTPU_Q_ROW | OTPU_Q_LO); ws: the hi rows' scale words Sw, srs apart.
+ *   nterms 3: hi.w_hi + lo.w_hi + hi.w_lo; nterms 2: hi.w_hi + hi.w_lo; each lo term's offsets
+ *   + 8 (dropped where 16 - da - 8 < 0); one exact integer an output and one fp32 epilogue
+ *   (i2f(acc) * Sw) * (Sa * 2^-16): the split product rounded once (not the sum of the separate
+ *   MMs).  flags: OTPU_RSC (required) and OTPU_ACC. */
+int otpu_mm_spl(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda, int M,
+                int nterms, const uint8_t* w, int64_t rs, int64_t hld, const uint8_t* ws, int64_t srs,
+                int N, int flags, float* out, int64_t ors, otpu_stream_t stream);
 
 /* The ACC fold of R rows of n (opentpu/isasim.py:899-905 applied in order): out = add(..add(
  * add(old | p_0, p_1)..), p_R-1) with FTZ adds, rows pstride apart; old may be NULL. */
@@ -145,9 +190,10 @@ int otpu_mm_batched(int B, const int8_t* q, int64_t ldq, int64_t q_bstride, cons
 
 /* LM head + greedy: one activation row (M = 1) times N vocabulary rows, the logits' total-order
  * maximum with the first index (opentpu/llm/qwen3.py:2052-2088 + opentpu/llm/generate.py:251-286
- * + VOP ARGMAX opentpu/isasim.py:1141-1152).  best = max over n of (key(y_n) << 32 | ~(base+n))
- * (a u64 whose low word is the complement of the index); token = base + that n.  logits may be
- * NULL. */
+ * + VOP ARGMAX opentpu/isasim.py:1141-1152).  best[0] = max over n of (key(y_n) << 32 |
+ * ~(base+n)) (a u64 whose low word is the complement of the index); token = base + that n.
+ * best[1] is the running maximum the GEMV's workgroups raise: zero before the first call (e.g.
+ * allocated zeroed), and every call leaves it zero again.  logits may be NULL.  Two kernels. */
 int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8_t* da, int K,
                         const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N,
                         int fmt, int flags, int k0, int64_t base, float* logits,
@@ -160,12 +206,13 @@ int otpu_argmax(const float* x, int rows, int cols, int64_t ldx, int64_t base, f
 
 /* Weight packers, bit-exact with opentpu/quant.py:quantize_mxu (no counterpart kernel in the
  * reference: it packs on the host in numpy).
- *   otpu_pack_int8: int8x (quant.py:316-322, rsc = 0; scale rows of 4 + 4*ceil(KB/4) bytes) or
- *   RSC rows (runtime.py:66-76 with row=True, rsc = 1; scale rows of 4 bytes).
+ *   otpu_pack_int8: int8x (quant.py:316-322, flags 0; scale rows of 4 + 4*ceil(KB/4) bytes) or
+ *   RSC rows (runtime.py:66-76 with row=True, flags OTPU_Q_ROW; scale rows of 4 bytes); with
+ *   OTPU_Q_LO the split's lo rows (QST LO: q8lo bytes, Sw * 2^-8; the weights' lo part of MM SPL).
  *   otpu_pack_x4: int4x / fp4x6 (quant.py:325-367; fmt OTPU_INT4 or OTPU_FP4) or nvfp4 with a
  *   per-row scale (quant.py:368-400; fmt OTPU_NVFP4): element rows of ceil(K/256)*128 bytes,
  *   scale rows of 8 + 8*ceil(KB/2) bytes (nvfp4: 16 + 16*ceil(KB/2)). */
-int otpu_pack_int8(const float* W, int N, int K, int64_t ldw, int rsc, uint8_t* rows,
+int otpu_pack_int8(const float* W, int N, int K, int64_t ldw, int flags, uint8_t* rows,
                    int64_t rs, uint8_t* srows, int64_t srs, otpu_stream_t stream);
 int otpu_pack_x4(const float* W, int N, int K, int64_t ldw, int fmt, uint8_t* rows, int64_t rs,
                  uint8_t* srows, int64_t srs, otpu_stream_t stream);
@@ -176,11 +223,15 @@ int otpu_pack_x4(const float* W, int N, int K, int64_t ldw, int fmt, uint8_t* ro
  * channel hash of hash_rows when at >= 0: the image's byte address on that machine, a multiple
  * of wg * 128) and of group_scales.  data: ceil(N / R) groups of grp_row_bytes (R = wg int8,
  * 2 wg 4-bit; wg = 1 the natural rows); rows: N rows of rs >= row_bytes(K); areas: the groups'
- * scale areas; srows: N scale rows of srs >= scale_bytes(K).  MM KT's pairs are not taken. */
-int otpu_ungroup_rows(const uint8_t* data, int N, int K, int wg, int fmt, int64_t at, uint8_t* rows,
-                      int64_t rs, otpu_stream_t stream);
-int otpu_ungroup_scales(const uint8_t* areas, int N, int K, int wg, int fmt, int rsc, uint8_t* srows,
-                        int64_t srs, otpu_stream_t stream);
+ * scale areas; srows: N scale rows of srs >= scale_bytes(K).  kt: the image is in MM KT's
+ * pairs (docs/isa.md "K tail", opentpu/quant.py:829-880: groups 2p and 2p + 1 share their last
+ * block's chunk, (2 KB - 1) chunks a pair; the odd groups' scale entries in chunk order, the tail
+ * block's first): K = KB D the padded K, the natural rows come out with block KB-1's upper half
+ * zero; int8, int4 and fp4 at wg > 1. */
+int otpu_ungroup_rows(const uint8_t* data, int N, int K, int wg, int fmt, int kt, int64_t at,
+                      uint8_t* rows, int64_t rs, otpu_stream_t stream);
+int otpu_ungroup_scales(const uint8_t* areas, int N, int K, int wg, int fmt, int rsc, int kt,
+                        uint8_t* srows, int64_t srs, otpu_stream_t stream);
 
 /* Checkpoint imports, exact (opentpu/quant.py:1070-1182, import_mxfp4 / import_nvfp4; the
  * reference converts on the host in numpy).  codes: one E2M1 code (0..15, sign bit 3) a byte,

@@ -16,13 +16,16 @@ LIB_PATH = os.environ.get("OTPU_LIB") or os.path.join(HERE, "libotpu_amd.so")
 INT8, INT4, FP4, NVFP4 = 0, 1, 2, 3
 FMT = {"int8": INT8, "int4": INT4, "fp4": FP4, "nvfp4": NVFP4}
 UNIT, ACC, RMAX, ASCALE, PAIR, RSC = 0x1, 0x2, 0x4, 0x8, 0x40, 0x80
+Q_ROW, Q_LO, Q_HL = 0x1, 0x10, 0x20             # QACT / QST flags
+QALIGN = 64                                     # QACT ST / LDA row alignment
 
 # every exported symbol and its argument types (P pointer, L int64, I int32, F float, D double)
 _P, _L, _I, _F, _D = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double
 SIGNATURES = {
     "otpu_last_error": ([], C.c_char_p),
     "otpu_version": ([], _I),
-    "otpu_qact": ([_P, _I, _I, _L, _I, _I, _P, _L, _P, _P, _L, _P], _I),
+    "otpu_qact": ([_P, _I, _I, _L, _I, _I, _P, _P, _P, _L, _P, _P, _L, _P, _L, _P], _I),
+    "otpu_lda": ([_P, _L, _I, _I, _P, _L, _P, _P, _L, _P], _I),
     "otpu_mm": ([_P, _L, _P, _P, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P, _P], _I),
     "otpu_mm_acc": ([_P, _L, _P, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P], _I),
     "otpu_mm_batched": ([_I, _P, _L, _L, _P, _L, _P, _L, _L, _I, _I, _P, _L, _L, _P, _L, _L, _I, _I, _I,
@@ -31,14 +34,15 @@ SIGNATURES = {
     "otpu_argmax": ([_P, _I, _I, _L, _L, _P, _L, _P], _I),
     "otpu_pack_int8": ([_P, _I, _I, _L, _I, _P, _L, _P, _L, _P], _I),
     "otpu_pack_x4": ([_P, _I, _I, _L, _I, _P, _L, _P, _L, _P], _I),
-    "otpu_qact_ranges": ([_P, _P, _I, _I, _L, _I, _I, _I, _P, _L, _P, _P, _L, _P], _I),
+    "otpu_qact_ranges": ([_P, _P, _I, _I, _L, _I, _I, _I, _P, _P, _P, _L, _P, _P, _L, _P], _I),
     "otpu_mm_ranges": ([_P, _L, _P, _P, _L, _I, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P], _I),
     "otpu_vmul": ([_P, _P, _P, _L, _P], _I),
-    "otpu_mm_qin": ([_P, _P, _I, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _L, _P], _I),
-    "otpu_mm_qin_fold": ([_P, _P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P], _I),
+    "otpu_mm_qin": ([_P, _P, _P, _P, _I, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _L, _P], _I),
+    "otpu_mm_qin_fold": ([_P, _P, _P, _P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P], _I),
+    "otpu_mm_spl": ([_P, _L, _P, _P, _L, _I, _I, _P, _L, _L, _P, _L, _I, _I, _P, _L, _P], _I),
     "otpu_acc_rows": ([_P, _I, _L, _I, _P, _P, _P], _I),
-    "otpu_ungroup_rows": ([_P, _I, _I, _I, _I, _L, _P, _L, _P], _I),
-    "otpu_ungroup_scales": ([_P, _I, _I, _I, _I, _I, _P, _L, _P], _I),
+    "otpu_ungroup_rows": ([_P, _I, _I, _I, _I, _I, _L, _P, _L, _P], _I),
+    "otpu_ungroup_scales": ([_P, _I, _I, _I, _I, _I, _I, _P, _L, _P], _I),
     "otpu_import_mxfp4": ([_P, _L, _P, _L, _I, _I, _I, _P, _L, _P, _L, _P, _P], _I),
     "otpu_import_nvfp4": ([_P, _L, _P, _L, _F, _I, _I, _P, _L, _P, _L, _P, _P], _I),
     "otpu_sample_work_bytes": ([_I], _L),

@@ -19,6 +19,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib as X
+from .mxu import C_ptr
 from .quant import D, quantize_mxu, row_bytes, scale_bytes
 
 
@@ -70,7 +71,12 @@ class DecodeChain:
     KERNELS_PER_LAYER = 9          # unfused: 3 QACT, 3 MM, QACT ranges, per-range MM + its ACC fold
     FUSED_KERNELS_PER_LAYER = 4    # fused: one QACT + MM kernel per linear
 
-    def __init__(self, layers: list, shape: Shape = Shape(), fmt: str = "int4", fused: bool = True):
+    def __init__(self, layers: list, shape: Shape = Shape(), fmt: str = "int4", fused: bool = True,
+                 norms: list | None = None):
+        """norms (optional): per layer (gamma_attn, gamma_mlp), the RMSNorm weights [hidden] in
+        front of the qkv and of the gate / up projections.  They ride in those linears' QACT as
+        CSCALE, with the row factor r of each norm (RSCALE: `self.rnorm[l, 0 | 1]`, 1 unless
+        the caller sets it): x' = (x * r) * gamma (`docs/isa.md:447-452`), no extra launch."""
         self.layers = layers
         self.shape = shape
         self.fmt = fmt
@@ -98,6 +104,12 @@ class DecodeChain:
         self.part = T.empty((self.R, s.hidden), dtype=f32, device=dev)
         self.parts = [T.zeros((self.R, s.hidden), dtype=f32, device=dev) for _ in range(2)]
         self.hbuf = [T.zeros((1, s.hidden), dtype=f32, device=dev) for _ in range(2)]
+        self.norms = None
+        if norms is not None:
+            if len(norms) != len(layers):
+                raise ValueError("DecodeChain: one (gamma_attn, gamma_mlp) pair a layer")
+            self.norms = [tuple(X.dev(g, np.float32).reshape(-1) for g in pair) for pair in norms]
+        self.rnorm = T.ones((len(layers), 2), dtype=f32, device=dev)
         self._graph = None
 
     @staticmethod
@@ -123,18 +135,25 @@ class DecodeChain:
         return DecodeChain(layers, shape, fmt, fused)
 
     @staticmethod
-    def from_packed(layers: list, shape: Shape = Shape(), fmt: str = "int4", fused: bool = True) -> "DecodeChain":
+    def from_packed(layers: list, shape: Shape = Shape(), fmt: str = "int4", fused: bool = True,
+                    norms: list | None = None) -> "DecodeChain":
         """Packed (rows, srows) pairs per layer (numpy or tensors), e.g. the reference's
         quantize_mxu output, loaded unchanged."""
         out = []
         for wts in layers:
             out.append({k: (X.dev(r, np.uint8), X.dev(sr, np.uint8)) for k, (r, sr) in wts.items()})
-        return DecodeChain(out, shape, fmt, fused)
+        return DecodeChain(out, shape, fmt, fused, norms)
 
     # --- the kernels of one step ---------------------------------------------------------
-    def _qact(self, x, K: int) -> None:
-        X.call("otpu_qact", X.ptr(x), 1, K, x.stride(0), 32, 0, X.ptr(self.qa), self.qa.shape[1],
-               X.ptr(self.Sa), X.ptr(self.da), self.da.shape[1], X.stream())
+    def _norm(self, l: int, i: int):
+        """(rscale, cscale) pointers of layer l's norm i (0: before qkv, 1: before gate / up)."""
+        if self.norms is None:
+            return None, None
+        return C_ptr(self.rnorm, 2 * l + i), X.ptr(self.norms[l][i])
+
+    def _qact(self, x, K: int, norm=(None, None)) -> None:
+        X.call("otpu_qact", X.ptr(x), 1, K, x.stride(0), 32, 0, norm[0], norm[1], X.ptr(self.qa), self.qa.shape[1],
+               X.ptr(self.Sa), X.ptr(self.da), self.da.shape[1], None, 0, X.stream())
 
     def _mm(self, w, K: int, out) -> None:
         rows, srows = w
@@ -145,46 +164,47 @@ class DecodeChain:
     def layer(self, l: int, x, y) -> None:
         """Queue layer l: input x [1, hidden] -> output y [1, hidden]."""
         s, w = self.shape, self.layers[l]
-        self._qact(x, s.hidden)
+        self._qact(x, s.hidden, self._norm(l, 0))
         self._mm(w["qkv"], s.hidden, self.qkv)
         self._qact(self.qkv, s.q_dim)                     # q: the first q_dim columns
         self._mm(w["o"], s.q_dim, self.o)
-        self._qact(self.o, s.hidden)
+        self._qact(self.o, s.hidden, self._norm(l, 1))
         self._mm(w["gu"], s.hidden, self.gu)
         g, u = self.gu[:, :s.F], self.gu[:, s.F:]
-        X.call("otpu_qact_ranges", X.ptr(g), X.ptr(u), 1, s.F, self.gu.shape[1], self.width, 32, 0, X.ptr(self.qa),
-               self.qa.shape[1], X.ptr(self.Sa), X.ptr(self.da), self.da.shape[1], X.stream())
+        X.call("otpu_qact_ranges", X.ptr(g), X.ptr(u), 1, s.F, self.gu.shape[1], self.width, 32, 0, None, None,
+               X.ptr(self.qa), self.qa.shape[1], X.ptr(self.Sa), X.ptr(self.da), self.da.shape[1], X.stream())
         rows, srows = w["down"]
         X.call("otpu_mm_ranges", X.ptr(self.qa), self.qa.shape[1], X.ptr(self.Sa), X.ptr(self.da),
                self.da.shape[1], 1, s.F, self.width, X.ptr(rows), rows.shape[1], X.ptr(srows), srows.shape[1],
                rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(self.part), X.ptr(y), y.shape[1], X.stream())
 
     def _qin(self, w, x, K: int, width: int, out, part_stride: int = 0, xmul=None, nsum: int = 1,
-             sum_stride: int = 0) -> None:
+             sum_stride: int = 0, norm=(None, None)) -> None:
         rows, srows = w
-        X.call("otpu_mm_qin", X.ptr(x), X.ptr(xmul), nsum, sum_stride, K, width, X.ptr(rows), rows.shape[1],
-               X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(out), rows.shape[0],
-               part_stride, X.stream())
+        X.call("otpu_mm_qin", X.ptr(x), X.ptr(xmul), norm[0], norm[1], nsum, sum_stride, K, width, X.ptr(rows),
+               rows.shape[1], X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(out),
+               rows.shape[0], part_stride, X.stream())
 
     def layer_fused(self, l: int, x, nsum: int, parts) -> None:
         """Queue layer l fused: input = the in-order fold of the nsum rows of x ([nsum, hidden]);
         output = the down projection's per-chunk rows in parts ([R, hidden], not yet folded)."""
         s, w = self.shape, self.layers[l]
-        self._qin(w["qkv"], x, s.hidden, s.hidden, self.qkv, nsum=nsum, sum_stride=s.hidden)
+        self._qin(w["qkv"], x, s.hidden, s.hidden, self.qkv, nsum=nsum, sum_stride=s.hidden, norm=self._norm(l, 0))
         self._qin(w["o"], self.qkv, s.q_dim, s.q_dim, self.o)
-        self._qin(w["gu"], self.o, s.hidden, s.hidden, self.gu)
+        self._qin(w["gu"], self.o, s.hidden, s.hidden, self.gu, norm=self._norm(l, 1))
         self._qin(w["down"], self.gu, s.F, self.width, parts, part_stride=s.hidden, xmul=self.gu[:, s.F:])
 
     def layer_folded(self, l: int, x, y) -> None:
         """Queue layer l fused, its down projection folded in one launch: input x [1, hidden] ->
         output y [1, hidden]."""
         s, w = self.shape, self.layers[l]
-        self._qin(w["qkv"], x, s.hidden, s.hidden, self.qkv)
+        self._qin(w["qkv"], x, s.hidden, s.hidden, self.qkv, norm=self._norm(l, 0))
         self._qin(w["o"], self.qkv, s.q_dim, s.q_dim, self.o)
-        self._qin(w["gu"], self.o, s.hidden, s.hidden, self.gu)
+        self._qin(w["gu"], self.o, s.hidden, s.hidden, self.gu, norm=self._norm(l, 1))
         rows, srows = w["down"]
-        X.call("otpu_mm_qin_fold", X.ptr(self.gu), X.ptr(self.gu[:, s.F:]), s.F, X.ptr(rows), rows.shape[1],
-               X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(y), X.stream())
+        X.call("otpu_mm_qin_fold", X.ptr(self.gu), X.ptr(self.gu[:, s.F:]), None, None, s.F, X.ptr(rows),
+               rows.shape[1], X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(y),
+               X.stream())
 
     @property
     def kernels_per_step(self) -> int:

@@ -32,8 +32,15 @@ __global__ void sum_parts(const float* __restrict__ part, int64_t pstride, int R
     *o = y;
 }
 
-__global__ void best_finish(const uint64_t* best, int32_t* token) {
-    if (threadIdx.x == 0) *token = (int32_t)~(uint32_t)(*best & 0xFFFFFFFFull);
+// the LM head's last step: the running maximum best[1] becomes the result best[0] and the
+// token, and is cleared for the next call (no fill launch before the GEMV)
+__global__ void best_finish(uint64_t* best, int32_t* token) {
+    if (threadIdx.x == 0) {
+        const uint64_t b = best[1];
+        best[0] = b;
+        best[1] = 0;
+        *token = (int32_t)~(uint32_t)(b & 0xFFFFFFFFull);
+    }
 }
 
 // VOP ARGMAX: one workgroup per row; (max, i2f(index + base))
@@ -256,9 +263,10 @@ extern "C" int otpu_mm_ranges(const int8_t* q, int64_t ldq, const float* Sa, con
     return otpu_launch_check("mm_ranges");
 }
 
-extern "C" int otpu_mm_qin(const float* x, const float* xmul, int nsum, int64_t sum_stride, int K, int width,
-                           const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
-                           int k0, float* out, int64_t ors, int64_t part_stride, otpu_stream_t stream) {
+extern "C" int otpu_mm_qin(const float* x, const float* xmul, const float* rscale, const float* cscale, int nsum,
+                           int64_t sum_stride, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
+                           int64_t srs, int N, int fmt, int flags, int k0, float* out, int64_t ors, int64_t part_stride,
+                           otpu_stream_t stream) {
     const int chunk = fmt == OTPU_INT8 ? OTPU_D : 2 * OTPU_D;
     if (width < chunk || width % chunk || K % width || width > QIN_KMAX)
         return otpu_fail(OTPU_EINVAL, "mm_qin: ranges of %d over K %d (multiples of %d, at most %d)", width, K, chunk,
@@ -267,8 +275,8 @@ extern "C" int otpu_mm_qin(const float* x, const float* xmul, int nsum, int64_t 
     if (!x || !out || nsum < 1 || nsum > QIN_NSUM_MAX || (nsum > 1 && sum_stride < K) || ors < N)
         return otpu_fail(OTPU_EINVAL, "mm_qin: x / out NULL, nsum %d, sum_stride %lld, ors %lld", nsum,
                          (long long)sum_stride, (long long)ors);
-    if (!al(x, 16) || (xmul && !al(xmul, 16)) || sum_stride % 4)
-        return otpu_fail(OTPU_EALIGN, "mm_qin: x and xmul 16-byte aligned, sum_stride a multiple of 4");
+    if (!al(x, 16) || (xmul && !al(xmul, 16)) || (cscale && !al(cscale, 16)) || sum_stride % 4)
+        return otpu_fail(OTPU_EALIGN, "mm_qin: x, xmul and cscale 16-byte aligned, sum_stride a multiple of 4");
     const int R = K / width;
     if (R > 1 && part_stride < N) return otpu_fail(OTPU_EINVAL, "mm_qin: part_stride %lld < N %d", (long long)part_stride, N);
     if (R > 65535) return otpu_fail(OTPU_EINVAL, "mm_qin: %d ranges", R);
@@ -281,6 +289,7 @@ extern "C" int otpu_mm_qin(const float* x, const float* xmul, int nsum, int64_t 
     MMArgs a = make_args(nullptr, width, nullptr, nullptr, width / 32, 1, width, w, rs, ws, srs, N, flags, k0);
     a.out = out; a.ors = ors; a.out_bs = part_stride;
     a.xin = x; a.xmul = xmul; a.nsum = nsum; a.sum_stride = sum_stride; a.xin_bs = width;
+    a.rscale = rscale; a.cscale = cscale;
     a.w_bs = fmt == OTPU_INT8 ? width : width / 2; a.k0_bs = plain ? 0 : width / OTPU_D;
     a.P = (fmt == OTPU_INT8 ? width : width / 2) / 16;
     int L = 1;
@@ -299,15 +308,16 @@ namespace otpu {
 void launch_fold(const MMArgs& a, int fmt, int L, hipStream_t s);   // gemv_fold.hip
 }
 
-extern "C" int otpu_mm_qin_fold(const float* x, const float* xmul, int K, const uint8_t* w, int64_t rs,
-                                const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0, float* out,
-                                otpu_stream_t stream) {
+extern "C" int otpu_mm_qin_fold(const float* x, const float* xmul, const float* rscale, const float* cscale, int K,
+                                const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
+                                int k0, float* out, otpu_stream_t stream) {
     if (fmt == OTPU_INT8) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: 4-bit weights (F-chunks of 256)");
     if (flags & ~OTPU_PAIR) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: no flags (weights with scale rows)");
     if (K < 256 || K % 256 || K > QIN_KMAX)
         return otpu_fail(OTPU_EINVAL, "mm_qin_fold: K %d (a multiple of 256, at most %d)", K, QIN_KMAX);
     if (!x || !out) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: x / out NULL");
-    if (!al(x, 16) || (xmul && !al(xmul, 16))) return otpu_fail(OTPU_EALIGN, "mm_qin_fold: x and xmul 16-byte aligned");
+    if (!al(x, 16) || (xmul && !al(xmul, 16)) || (cscale && !al(cscale, 16)))
+        return otpu_fail(OTPU_EALIGN, "mm_qin_fold: x, xmul and cscale 16-byte aligned");
     int rc = check_mm("mm_qin_fold", reinterpret_cast<const int8_t*>(x), K, reinterpret_cast<const uint8_t*>(x),
                       K / 32, 1, K, w, rs, ws, srs, N, fmt, flags, k0);
     if (rc) return rc;
@@ -315,6 +325,7 @@ extern "C" int otpu_mm_qin_fold(const float* x, const float* xmul, int K, const 
     MMArgs a = make_args(nullptr, K, nullptr, nullptr, K / 32, 1, K, w, rs, ws, srs, N, flags & ~OTPU_PAIR, k0);
     a.out = out; a.ors = N;
     a.xin = x; a.xmul = xmul; a.nsum = 1;
+    a.rscale = rscale; a.cscale = cscale;
     a.P = (K / 2) / 16;
     int L = 1;
     pick_team(a.P, &a.T, &L);
@@ -346,11 +357,10 @@ extern "C" int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8
     if (rc) return rc;
     if (!Sa || !best || !token) return otpu_fail(OTPU_EINVAL, "lm_head_argmax: NULL Sa, best or token");
     if (base < 0 || base + (int64_t)N > 0xFFFFFFFFll) return otpu_fail(OTPU_EINVAL, "lm_head_argmax: base %lld", (long long)base);
-    if (!al(best, 8)) return otpu_fail(OTPU_EALIGN, "lm_head_argmax: best 8-byte aligned");
+    if (!al(best, 16)) return otpu_fail(OTPU_EALIGN, "lm_head_argmax: best (two words) 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     MMArgs a = make_args(q, K, Sa, da, K / 32, 1, K, w, rs, ws, srs, N, flags, k0);
-    a.out = logits; a.ors = N; a.best = best; a.base = base;
-    fill_u32<<<1, 64, 0, s>>>(reinterpret_cast<uint32_t*>(best), 2, 0u);
+    a.out = logits; a.ors = N; a.best = best + 1; a.base = base;
     rc = launch_gemv(a, fmt, 1, s);
     if (rc) return rc;
     best_finish<<<1, 64, 0, s>>>(best, token);

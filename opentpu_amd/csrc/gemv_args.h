@@ -28,9 +28,12 @@ struct MMArgs {
     int64_t q_bs, sa_bs, da_bs, w_bs, ws_bs, out_bs;
     int k0_bs;
     // QACT in the prologue (one activation row): the fp32 row xin (problem b at + b * xin_bs),
-    // the fold of nsum rows sum_stride apart, times xmul when given
+    // the fold of nsum rows sum_stride apart, times xmul when given, then times rscale[0]
+    // (RSCALE) and cscale[column] (CSCALE) when given
     const float* xin;
     const float* xmul;
+    const float* rscale;
+    const float* cscale;
     int nsum;
     int64_t sum_stride, xin_bs;
 };

@@ -59,15 +59,18 @@ __device__ __forceinline__ void fold_body(const MMArgs& a) {
     };
 
     // 1. the input row's loads, then the first row's weights (loads complete in order)
-    float4 xv[CPT], gv[CPT];
+    float4 xv[CPT], gv[CPT], cv[CPT];
+    const float4* cs = reinterpret_cast<const float4*>(a.cscale);
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
         const int c = tid + 256 * k;
         if (c < NC) {
             xv[k] = reinterpret_cast<const float4*>(x)[c];
             if (xm) gv[k] = reinterpret_cast<const float4*>(xm)[c];
+            if (cs) cv[k] = cs[c];
         }
     }
+    const float rf = a.rscale ? *a.rscale : 1.0f;
     Stage st;
     const int nfirst = wave * NT + team;
     __builtin_amdgcn_sched_barrier(0);
@@ -87,6 +90,10 @@ __device__ __forceinline__ void fold_body(const MMArgs& a) {
             t = xv[k];
             if (xm) {                                    // VOP MUL
                 t.x = fmul(t.x, gv[k].x); t.y = fmul(t.y, gv[k].y); t.z = fmul(t.z, gv[k].z); t.w = fmul(t.w, gv[k].w);
+            }
+            if (a.rscale) { t.x = fmul(t.x, rf); t.y = fmul(t.y, rf); t.z = fmul(t.z, rf); t.w = fmul(t.w, rf); }
+            if (cs) {                                    // RSCALE, then CSCALE: (x * r) * c
+                t.x = fmul(t.x, cv[k].x); t.y = fmul(t.y, cv[k].y); t.z = fmul(t.z, cv[k].z); t.w = fmul(t.w, cv[k].w);
             }
             t.x = ftz(t.x); t.y = ftz(t.y); t.z = ftz(t.z); t.w = ftz(t.w);
         }

@@ -167,7 +167,8 @@ __device__ __forceinline__ double xsum(double x, int o) {
 
 // QACT of the problem's fp32 row in the prologue (fp32.quantize_mx(x, 32) of one row, as
 // qact_kernel computes it), once per workgroup: each thread takes float4 chunks of the row
-// (folding nsum partial rows in order, times xmul when given), the workgroup finds the row
+// (folding nsum partial rows in order, times xmul when given, then QACT's RSCALE and CSCALE
+// products when given), the workgroup finds the row
 // maximum, each 32-group's 8 threads its group maximum (xor exchanges), and the quantized
 // bytes and group offsets go to LDS; then every lane reads its own pieces (4-bit layouts:
 // even / odd elements split, as the loaded path permutes them).
@@ -187,9 +188,24 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
     const int tid = threadIdx.x;
     const float* x = a.xin + b * a.xin_bs;
     const float* xm = a.xmul ? a.xmul + b * a.xin_bs : nullptr;
-    float4 v[CPT];
+    const float4* cs = a.cscale ? reinterpret_cast<const float4*>(a.cscale + b * a.xin_bs) : nullptr;
+    float4 v[CPT], cv[CPT];
+    float rf = 1.0f;
     uint32_t m = 0;
-    auto finish = [&](float4 t, int k) {                 // VOP MUL done: flush, keep, row max
+    // RSCALE / CSCALE factors, loaded with the row (QACT's pre-multiplies: (x * r) * c)
+    auto load_scales = [&]() {
+        if (a.rscale) rf = *a.rscale;
+        if (cs) {
+#pragma unroll
+            for (int k = 0; k < CPT; ++k) {
+                const int c = tid + 256 * k;
+                if (c < NC) cv[k] = cs[c];
+            }
+        }
+    };
+    auto finish = [&](float4 t, int k) {                 // VOP MUL done: pre-multiplies, flush, keep, row max
+        if (a.rscale) { t.x = fmul(t.x, rf); t.y = fmul(t.y, rf); t.z = fmul(t.z, rf); t.w = fmul(t.w, rf); }
+        if (cs) { t.x = fmul(t.x, cv[k].x); t.y = fmul(t.y, cv[k].y); t.z = fmul(t.z, cv[k].z); t.w = fmul(t.w, cv[k].w); }
         t.x = ftz(t.x); t.y = ftz(t.y); t.z = ftz(t.z); t.w = ftz(t.w);
         v[k] = t;
         m = max(m, max(max(fbits(t.x) & 0x7FFFFFFFu, fbits(t.y) & 0x7FFFFFFFu),
@@ -205,6 +221,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
                 if (xm) gv[k] = reinterpret_cast<const float4*>(xm)[c];
             }
         }
+        load_scales();
         __builtin_amdgcn_sched_barrier(0);
         issue_weights();
         __builtin_amdgcn_sched_barrier(0);
@@ -223,6 +240,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
         }
     } else {
     issue_weights();
+    load_scales();
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
         const int c = tid + 256 * k;

@@ -75,6 +75,7 @@ __device__ __forceinline__ float step01(float x) { return tmin(tmax(fmul(x, 0x1p
 struct SampleArgs {
     const float* logits;
     int V, nb;
+    int vec4;                     // logits 16-byte aligned and V a multiple of 4: float4 loads
     const float* pa;              // penalty factors (NULL: none)
     const float* pb;
     int cap;                      // soft cap on
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(256) void sample_blocks(SampleArgs a) {
     float l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) l[j] = __uint_as_float(0xFF800000u);   // -inf past V
-    if (ok && i0 + 3 < a.V && (a.V & 3) == 0) {
+    if (ok && i0 + 3 < a.V && a.vec4) {          // (logits 16-byte aligned and V a multiple of 4)
         const float4 v = *reinterpret_cast<const float4*>(a.logits + i0);
         l[0] = v.x;
         l[1] = v.y;
@@ -479,6 +480,7 @@ extern "C" int otpu_sample(const float* logits, int V, const float* pa, const fl
     SampleArgs a;
     a.logits = logits;
     a.V = V;
+    a.vec4 = (V & 3) == 0 && ((uintptr_t)logits & 15) == 0;
     a.nb = (V + SBLK - 1) / SBLK;
     a.pa = pa;
     a.pb = pb;

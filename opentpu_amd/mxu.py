@@ -63,6 +63,26 @@ def mm_acc(q, da, rows, srows, fmt: str, K: int, *, rsc: bool = False, unit: boo
     return X.host(acc) if numpy_in else acc
 
 
+def mm_spl(q, Sa, da, w_hi, w_lo, Sw, nterms: int, *, acc=None):
+    """MM SPL (`opentpu/isasim.py:757-770`, `docs/isa.md:414-441`): one MM over a split
+    operand's terms, one 128-block of int8 RSC weights a part.  q int8 [M, 128] (2 terms) or
+    [M, 256] (3 terms: hi then lo, as `fp32.qact(hl=True)` gives them side by side), Sa [M] and
+    da [M, 4] the hi part's, w_hi / w_lo the weights' hi and lo rows [N, 128] (`quantize_mxu(W,
+    "int8", rsc=True)` and `(..., lo=True)`), Sw [N] the hi rows' scales.  acc: ACC into it."""
+    numpy_in = X.is_numpy(q)
+    qd = X.dev(q, np.int8)
+    Sad, dad = X.dev(Sa, np.float32), X.dev(da, np.uint8)
+    wh, wl = X.dev(w_hi, np.uint8), X.dev(w_lo, np.uint8)
+    M, N = qd.shape[0], wh.shape[0]
+    T = X.torch()
+    w = T.cat([wh[:, :D], wl[:, :D]], 1).contiguous()     # hi rows, each followed by its lo row
+    ws = X.dev(np.asarray(Sw, np.float32).reshape(-1) if X.is_numpy(Sw) else Sw, np.float32)
+    out = X.empty((M, N), np.float32) if acc is None else X.dev(acc, np.float32).clone()
+    X.call("otpu_mm_spl", X.ptr(qd), qd.shape[1], X.ptr(Sad), X.ptr(dad), dad.shape[1], M, nterms, X.ptr(w),
+           2 * D, D, X.ptr(ws), 4, N, RSC | (ACC if acc is not None else 0), X.ptr(out), N, X.stream())
+    return X.host(out) if numpy_in else out
+
+
 def lm_head_argmax(q, Sa, da, rows, srows, fmt: str, K: int, *, rsc: bool = False, k0: int = 0,
                    base: int = 0, logits: bool = True):
     """One activation row times the vocabulary rows, with the greedy pick fused: returns
@@ -72,7 +92,7 @@ def lm_head_argmax(q, Sa, da, rows, srows, fmt: str, K: int, *, rsc: bool = Fals
     wd, sd = X.dev(rows, np.uint8), X.dev(srows, np.uint8)
     N = wd.shape[0]
     lg = X.empty((N,), np.float32) if logits else None
-    best = X.empty((1,), np.int64)
+    best = X.zeros((2,), np.int64)                 # the result word, the running maximum (zero)
     tok = X.empty((1,), np.int32)
     X.call("otpu_lm_head_argmax", X.ptr(qd), X.ptr(Sad), X.ptr(dad), K, X.ptr(wd), wd.shape[1], X.ptr(sd),
            sd.shape[1], N, X.FMT[fmt], _flags(rsc=rsc), k0, base, X.ptr(lg), X.ptr(best), X.ptr(tok),
@@ -80,7 +100,7 @@ def lm_head_argmax(q, Sa, da, rows, srows, fmt: str, K: int, *, rsc: bool = Fals
     if numpy_in:
         return (int(X.host(tok)[0]), X.host(lg) if logits else None,
                 int(X.host(best).view(np.uint64)[0]))
-    return tok, lg, best
+    return tok, lg, best[:1]
 
 
 def argmax(x, base: int = 0):
@@ -144,8 +164,8 @@ def quantize_ranges(x, ranges=None, row_mode: bool = False):
     c0 = 0
     for i, w in enumerate(ranges):
         xs = xd[:, c0:c0 + w]
-        X.call("otpu_qact", X.ptr(xs), M, w, K, 32, int(bool(row_mode)), C_ptr(q, c0), K, X.ptr(Sa[i]),
-               C_ptr(da, c0 // 32), K // 32, X.stream())
+        X.call("otpu_qact", X.ptr(xs), M, w, K, 32, X.Q_ROW if row_mode else 0, None, None, C_ptr(q, c0), K,
+               X.ptr(Sa[i]), C_ptr(da, c0 // 32), K // 32, None, 0, X.stream())
         c0 += w
     del T
     return q, Sa, da, ranges
@@ -225,5 +245,5 @@ def greedy(x, w: QWeight, chunk: int | None = None) -> int:
     return g.token()
 
 
-__all__ = ["mm", "mm_acc", "lm_head_argmax", "argmax", "QWeight", "quantize_ranges", "dot", "Greedy",
+__all__ = ["mm", "mm_acc", "mm_spl", "lm_head_argmax", "argmax", "QWeight", "quantize_ranges", "dot", "Greedy",
            "greedy", "UNIT", "ACC", "RMAX", "ASCALE", "RSC", "WINDOW"]

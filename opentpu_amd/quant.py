@@ -34,13 +34,18 @@ def scale_bytes(K: int, fmt: str, rsc: bool = False) -> int:
     raise ValueError(f"unknown MXU format {fmt!r}")
 
 
-def quantize_mxu(W, fmt: str, rsc: bool = False):
+def quantize_mxu(W, fmt: str, D: int = D, *, rsc: bool = False, lo: bool = False):
     """W [N, K] fp32 -> (element rows uint8 [N, row_bytes], scale rows uint8 [N, scale_bytes]),
-    packed on the GPU.  fmt "int8" (int8x; with rsc=True the RSC rows of one fp32 scale each,
-    `opentpu/runtime.py:66-76`), "int4", "fp4" or "nvfp4" (`opentpu/quant.py:368-400`).  numpy
-    in, numpy out; tensors stay on the device."""
+    packed on the GPU (`opentpu/quant.py:510-523`; D the MXU depth, 128 on this path).  fmt
+    "int8" (int8x; with rsc=True the RSC rows of one fp32 scale each, `opentpu/runtime.py:66-76`;
+    with lo=True also the split's lo rows, QST LO: q8lo bytes and Sw * 2^-8), "int4", "fp4" or
+    "nvfp4" (`opentpu/quant.py:368-400`).  numpy in, numpy out; tensors stay on the device."""
     if fmt not in MXU_FORMATS:
         raise ValueError(f"quantize_mxu: unknown MXU format {fmt!r}")
+    if D != 128:
+        raise ValueError(f"quantize_mxu: D {D}: the MM kernels stream blocks of 128")
+    if lo and fmt != "int8":
+        raise ValueError("quantize_mxu: the split's lo rows are int8")
     numpy_in = X.is_numpy(W)
     Wd = X.dev(W, np.float32)
     N, K = Wd.shape
@@ -49,8 +54,8 @@ def quantize_mxu(W, fmt: str, rsc: bool = False):
     rows = X.empty((N, rb), np.uint8)
     srows = X.empty((N, srs), np.uint8)
     if fmt == "int8":
-        X.call("otpu_pack_int8", X.ptr(Wd), N, K, K, int(bool(rsc)), X.ptr(rows), rb, X.ptr(srows), srs,
-               X.stream())
+        fl = (X.Q_ROW if rsc else 0) | (X.Q_LO if lo else 0)
+        X.call("otpu_pack_int8", X.ptr(Wd), N, K, K, fl, X.ptr(rows), rb, X.ptr(srows), srs, X.stream())
     else:
         if rsc:
             raise ValueError("quantize_mxu: RSC rows are int8")
@@ -64,7 +69,8 @@ def quantize_mxu(W, fmt: str, rsc: bool = False):
 # 4-bit, 1 at WG = 1), optionally with its chunks' lanes in the channel hash's order at the
 # image's address (`docs/isa.md` "Weight groups"; `opentpu/quant.py:634-808`, `grouped`). The
 # converters below turn such an image back into the natural rows every MM entry point streams,
-# on the GPU (`otpu_ungroup_rows`, `otpu_ungroup_scales`). MM KT's pairs are not taken.
+# on the GPU (`otpu_ungroup_rows`, `otpu_ungroup_scales`), MM KT's pairs included (`kt=True`:
+# `opentpu/quant.py:829-880`, the natural rows of the padded K).
 
 def grp_r(fmt: str, wg: int) -> int:
     """Rows of a group on a machine of wg lanes."""
@@ -97,41 +103,57 @@ def _check_image(a, G: int, width: int, what: str):
         raise ValueError(f"{what}: expected a contiguous [{G}, {width}] uint8 image, got {tuple(a.shape)}")
 
 
-def ungroup_rows(data, N: int, K: int, wg: int, fmt: str, at: int | None = None):
+def kt_pair_bytes(K: int, fmt: str, wg: int) -> int:
+    """The pair stride of a [., K] matrix in MM KT's pairs: (2 KB - 1) P (`opentpu/quant.py:836-839`)."""
+    return 2 * grp_row_bytes(K, fmt, wg) - wg * D
+
+
+def ungroup_rows(data, N: int, K: int, wg: int, fmt: str, at: int | None = None, kt: bool = False):
     """A grouped element image [ceil(N / R), grp_row_bytes] (uint8; `at`: its byte address on a
-    machine with the channel hash, None: unhashed) -> natural rows [N, row_bytes] on the GPU.
-    numpy in, numpy out."""
+    machine with the channel hash, None: unhashed; kt: in MM KT's pairs, [ceil(G / 2),
+    kt_pair_bytes], K the padded K) -> natural rows [N, row_bytes] on the GPU.  numpy in, numpy
+    out."""
     if fmt not in MXU_FORMATS:
         raise ValueError(f"unknown MXU format {fmt!r}")
+    if kt and (wg == 1 or fmt == "nvfp4"):
+        raise ValueError("ungroup_rows: KT's pairs are of groups (wg > 1) of int8, int4 or fp4")
     numpy_in = X.is_numpy(data)
     d = X.dev(data, np.uint8)
     G = -(-N // grp_r(fmt, wg))
-    _check_image(d, G, grp_row_bytes(K, fmt, wg), "ungroup_rows")
+    if kt:
+        _check_image(d, -(-G // 2), kt_pair_bytes(K, fmt, wg), "ungroup_rows")
+    else:
+        _check_image(d, G, grp_row_bytes(K, fmt, wg), "ungroup_rows")
     rows = X.empty((N, row_bytes(K, fmt)), np.uint8)
-    X.call("otpu_ungroup_rows", X.ptr(d), N, K, wg, X.FMT[fmt], -1 if at is None else int(at), X.ptr(rows),
-           rows.shape[1], X.stream())
+    X.call("otpu_ungroup_rows", X.ptr(d), N, K, wg, X.FMT[fmt], int(bool(kt)), -1 if at is None else int(at),
+           X.ptr(rows), rows.shape[1], X.stream())
     return X.host(rows) if numpy_in else rows
 
 
-def ungroup_scales(areas, N: int, K: int, wg: int, fmt: str, rsc: bool = False):
-    """Grouped scale areas [ceil(N / R), grp_scale_bytes] -> natural scale rows [N, scale_bytes]
-    on the GPU (reserved words and padding 0). numpy in, numpy out."""
+def ungroup_scales(areas, N: int, K: int, wg: int, fmt: str, rsc: bool = False, kt: bool = False):
+    """Grouped scale areas [ceil(N / R), grp_scale_bytes] (kt: MM KT's, the odd groups' entries
+    in chunk order) -> natural scale rows [N, scale_bytes] on the GPU (reserved words and
+    padding 0). numpy in, numpy out."""
     if fmt not in MXU_FORMATS:
         raise ValueError(f"unknown MXU format {fmt!r}")
+    if kt and (wg == 1 or fmt == "nvfp4"):
+        raise ValueError("ungroup_scales: KT's pairs are of groups (wg > 1) of int8, int4 or fp4")
     numpy_in = X.is_numpy(areas)
     a = X.dev(areas, np.uint8)
     G = -(-N // grp_r(fmt, wg))
     _check_image(a, G, grp_scale_bytes(K, fmt, wg, rsc), "ungroup_scales")
     srows = X.empty((N, scale_bytes(K, fmt, rsc)), np.uint8)
-    X.call("otpu_ungroup_scales", X.ptr(a), N, K, wg, X.FMT[fmt], int(bool(rsc)), X.ptr(srows), srows.shape[1],
-           X.stream())
+    X.call("otpu_ungroup_scales", X.ptr(a), N, K, wg, X.FMT[fmt], int(bool(rsc)), int(bool(kt)), X.ptr(srows),
+           srows.shape[1], X.stream())
     return X.host(srows) if numpy_in else srows
 
 
-def ungrouped(data, areas, N: int, K: int, wg: int, fmt: str, at: int | None = None, rsc: bool = False):
-    """The inverse of the reference's `quant.grouped(q, s, fmt, K, wg, at=at)` without KT
-    (`opentpu/quant.py:811-826`): an image's (data, scale areas) -> (rows, scale rows) for MM."""
-    return ungroup_rows(data, N, K, wg, fmt, at), ungroup_scales(areas, N, K, wg, fmt, rsc)
+def ungrouped(data, areas, N: int, K: int, wg: int, fmt: str, at: int | None = None, rsc: bool = False,
+              kt: bool = False):
+    """The inverse of the reference's `quant.grouped(q, s, fmt, K, wg, at=at, kt=kt)`
+    (`opentpu/quant.py:811-826`): an image's (data, scale areas) -> (rows, scale rows) for MM
+    (with kt, K is the padded K: a whole number of blocks)."""
+    return ungroup_rows(data, N, K, wg, fmt, at, kt), ungroup_scales(areas, N, K, wg, fmt, rsc, kt)
 
 
 # -------------------------------------------------------------------------- checkpoint imports

@@ -21,17 +21,22 @@ class Sampling:
 
     def __init__(self, temperature: float, top_k: int, top_p: float = 1.0,
                  repetition_penalty: float = 1.0):
-        greedy = temperature <= 0 or top_p < TOPP_MIN
-        if not greedy and not 0 < top_k <= K_MAX:
-            raise ValueError(f"the sampler on the device takes top_k 1 .. {K_MAX}")
+        # a non-positive temperature, or a top_p that flushes to zero, picks the largest logit:
+        # one candidate, unit scale, no top-p cut
+        self.greedy = temperature <= 0 or top_p < TOPP_MIN
         if repetition_penalty < 1.0:
-            raise ValueError("the sampler on the device takes repetition_penalty >= 1")
-        self.k = 1 if greedy else int(top_k)
-        self.itemp = 1.0 if greedy else math.log2(math.e) / temperature
-        self.top_p = 1.0 if greedy else float(top_p)
+            raise ValueError(f"Sampling: repetition_penalty {repetition_penalty} is below 1")
+        if self.greedy:
+            self.k, self.itemp, self.top_p = 1, 1.0, 1.0
+        else:
+            if not 1 <= top_k <= K_MAX:
+                raise ValueError(f"Sampling: top_k {top_k} outside 1 .. {K_MAX}")
+            self.k = int(top_k)
+            self.itemp = math.log2(math.e) / temperature       # exp2 of logit * itemp = exp(logit / T)
+            self.top_p = float(top_p)
         self.penalty = float(repetition_penalty)
-        self.kmax = -(-self.k // 8) * 8
         self.pen = self.penalty != 1.0
+        self.kmax = 8 * -(-self.k // 8)                        # candidate buffers in whole 8s
 
 
 def penalty_factors(V: int, context, R: float):

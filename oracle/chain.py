@@ -12,6 +12,13 @@ One layer, restated from the reference's lowering of a decoder layer's linears:
     `opentpu/compiler.py:2686-2720`);
   - the next layer's input is the down projection's output.
 
+`emulated_layer` is the same layer in float64 with the quantization points but none of the
+machine's rounding, the way the reference separates quantization error from kernel bugs
+(`opentpu/llm/qwen3.py:830-905` emulated_logits, `opentpu/reference.py:14-17` mlp): each
+linear's input through `emulate.fake_act` (its QACT ranges: the whole row, the down input in its
+F-chunks), the weights through `emulate.fake_w`, each product through `emulate.mx_matmul` (the
+window's drops), g * u a float64 product.
+
 Pinning (tests/test_oracle_chain.py): `down_chunk` against the closed form of
 `opentpu/kernels/mlp.py:8-30` and the chunk sizes the reference documents for F = 3072 (int8
 384, 4-bit 256); the per-range ACC chain against one MM over the whole row where one range
@@ -22,9 +29,10 @@ from __future__ import annotations
 
 import numpy as np
 
+from . import emulate as EM
 from . import fp32 as F
 from . import mm as MM
-from .formats import D
+from .formats import D, WINDOW
 
 ACC = MM.ACC
 
@@ -49,10 +57,11 @@ def down_chunk(f_loc: int, fmt: str) -> int:
     return chunk(f_loc, D if fmt == "int8" else 2 * D)
 
 
-def linear(x, w, fmt: str):
-    """QACT of x [M, K] (one range) and the MM with packed weights w = (rows, srows)."""
+def linear(x, w, fmt: str, rscale=None, cscale=None):
+    """QACT of x [M, K] (one range; with QACT's RSCALE / CSCALE factors when given) and the MM
+    with packed weights w = (rows, srows)."""
     x = np.asarray(x, np.float32)
-    q, Sa, da = F.quantize_mx(x, 32)
+    q, Sa, da = F.qact(x, 32, rscale=rscale, cscale=cscale)
     return MM.mm(q, Sa, da, w[0], w[1], fmt, x.shape[1])
 
 
@@ -73,19 +82,43 @@ def ranges_dot(x, w, fmt: str, width: int):
     return y
 
 
-def layer(x, wts: dict, fmt: str = "int4", q_dim: int = 2048, F_dim: int = 3072):
+def layer(x, wts: dict, fmt: str = "int4", q_dim: int = 2048, F_dim: int = 3072, norm=None):
     """One layer's linears: wts holds packed (rows, srows) for 'qkv' (q, k, v rows stacked),
-    'o', 'gu' (gate, up rows stacked) and 'down'.  Returns (next input, dict of the outputs)."""
-    qkv = linear(x, wts["qkv"], fmt)
+    'o', 'gu' (gate, up rows stacked) and 'down'.  norm (optional): (gamma_attn, gamma_mlp,
+    r_attn, r_mlp), the RMSNorm factors the qkv and gate / up QACTs apply (RSCALE r, CSCALE
+    gamma).  Returns (next input, dict of the outputs)."""
+    g0, g1, r0, r1 = norm if norm is not None else (None, None, None, None)
+    qkv = linear(x, wts["qkv"], fmt, r0, g0)
     o = linear(qkv[:, :q_dim], wts["o"], fmt)
-    gu = linear(o, wts["gu"], fmt)
+    gu = linear(o, wts["gu"], fmt, r1, g1)
     h = F.mul(gu[:, :F_dim], gu[:, F_dim:2 * F_dim])
     y = ranges_dot(h, wts["down"], fmt, down_chunk(F_dim, fmt))
     return y, {"qkv": qkv, "o": o, "gu": gu, "h": h, "down": y}
 
 
-def step(x, layers: list, fmt: str = "int4", q_dim: int = 2048, F_dim: int = 3072):
+def step(x, layers: list, fmt: str = "int4", q_dim: int = 2048, F_dim: int = 3072, norms=None):
     """The decode step: every layer in order; returns the last layer's output."""
-    for wts in layers:
-        x, _ = layer(x, wts, fmt, q_dim, F_dim)
+    for i, wts in enumerate(layers):
+        x, _ = layer(x, wts, fmt, q_dim, F_dim, norms[i] if norms is not None else None)
     return x
+
+
+def emulated_linear(x, w, fmt: str, n: int | None = None):
+    """float64: fake_act of x [M, K] (ranges of n columns) times fake_w of w = (rows, srows) with
+    MM's window drops."""
+    x = np.asarray(x, np.float64)
+    K = x.shape[1]
+    h, da = EM.fake_act(x, n=n)
+    wv, dw = EM.fake_w(w[0], w[1], fmt, K)
+    return EM.mx_matmul(h, wv, da, dw, WINDOW[fmt])
+
+
+def emulated_layer(x, wts: dict, fmt: str = "int4", q_dim: int = 2048, F_dim: int = 3072):
+    """One layer in float64 with the quantization points (see the module's header): (output,
+    dict of the intermediates)."""
+    qkv = emulated_linear(x, wts["qkv"], fmt)
+    o = emulated_linear(qkv[:, :q_dim], wts["o"], fmt)
+    gu = emulated_linear(o, wts["gu"], fmt)
+    h = gu[:, :F_dim] * gu[:, F_dim:2 * F_dim]
+    y = emulated_linear(h, wts["down"], fmt, down_chunk(F_dim, fmt))
+    return y, {"qkv": qkv, "o": o, "gu": gu, "h": h, "down": y}

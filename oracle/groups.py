@@ -14,9 +14,21 @@ fold of A / P into log2 WG bits. Group g's scale area (grp_scale_bytes apart): r
 at 4 j, then from SWP on block k's data of row j (SB bytes: int8 1, int4 / fp4 4, NVFP4 8, RSC
 none) at SWP + (k R + j) SB.
 
+MM KT's pairs (`docs/isa.md` "K tail", `opentpu/quant.py:829-880`: kt_rows, kt_scales): a
+grouped matrix whose K ends in the first half of its last block (the upper half of every lane's
+last chunk zero) is stored as pairs of groups, (2 KB - 1) P bytes a pair: group 2p's chunks
+0 .. KB-2, the tail chunk (each lane's D bytes: group 2p's half block, then group 2p + 1's),
+group 2p + 1's chunks 0 .. KB-2 (an odd group count's last pair: group 2p alone, its tail's
+other half zero).  The odd groups' scale entries are stored in the order the MXU takes their
+chunks: the tail block's entry first, then blocks 0 .. KB-2; a 4-bit tail entry's sub-block 0
+and 1 multipliers are also copied over those of sub-blocks 2 and 3 (which meet zeros).
+
 The functions below build every map one byte address at a time from those formulas (the
 reference reshapes whole arrays), so a transposed axis or a wrong stride shows up as a byte in
-the wrong place. Pinning (tests/test_oracle_groups.py): the chunk fold's known answer
+the wrong place. Pinning (tests/test_oracle_groups.py): KT: the pair stride and one chunk saved
+a pair (the reference's `tests/test_kt.py:115-124` and `:177-200` restated with own inputs),
+every chunk of a pair against the layout's formula, refusal of a non-zero upper half, and
+ungroup(kt pairs) = the natural rows, byte for byte; the chunk fold's known answer
 (0b100_011_110 at R 8 folds to 1; R 1 folds to 0) from the reference's
 `tests/test_wg.py:125-137`; the scale-area offsets and 4-bit chunk layout checks of
 `tests/test_wg.py:178-216` restated with their own inputs; WG = 1 the natural layout byte for
@@ -137,6 +149,113 @@ def hash_rows(data, at: int, wg: int) -> np.ndarray:
             dst = m * P + (l ^ h) * D
             out[dst:dst + D] = flat[m * P + l * D:m * P + (l + 1) * D]
     return out.reshape(data.shape)
+
+
+def kt_rows(data, wg: int) -> np.ndarray:
+    """Grouped bytes [G, KB P] whose last chunk's upper lane halves are zero -> MM KT's pairs
+    [ceil(G / 2), (2 KB - 1) P] (`opentpu/quant.py:842-858`), chunk by chunk."""
+    data = np.asarray(data, np.uint8)
+    P = wg * D
+    G = data.shape[0]
+    KB = data.shape[1] // P
+    ch = data.reshape(G, KB, wg, D)
+    if np.any(ch[:, KB - 1, :, D // 2:]):
+        raise ValueError("kt_rows: the last K-block's upper halves are not zero")
+    pairs = -(-G // 2)
+    out = np.zeros((pairs, (2 * KB - 1) * P), np.uint8)
+    for p in range(pairs):
+        for e in (0, 1):
+            g = 2 * p + e
+            if g >= G:
+                continue
+            for c in range(KB - 1):                              # whole chunks
+                at = (c if e == 0 else KB + c) * P
+                out[p, at:at + P] = data[g, c * P:(c + 1) * P]
+            for l in range(wg):                                  # the tail chunk's lane halves
+                at = (KB - 1) * P + l * D + e * (D // 2)
+                out[p, at:at + D // 2] = ch[g, KB - 1, l, :D // 2]
+    return out
+
+
+def kt_group_chunk(g: int, c: int, KB: int) -> tuple:
+    """Where group g's chunk c lies in MM KT's pairs: (chunk index from the image's start, the
+    byte in each lane where its D / 2 bytes start for the tail chunk c = KB - 1, else 0)."""
+    p, e = divmod(g, 2)
+    if c < KB - 1:
+        return p * (2 * KB - 1) + e * KB + c, 0
+    return p * (2 * KB - 1) + KB - 1, e * (D // 2)
+
+
+def ungroup_kt_rows(data, N: int, K: int, fmt: str, wg: int, at: int | None = None) -> np.ndarray:
+    """MM KT's pairs (hashed as stored at `at` when given) -> natural rows [N, row_bytes(K)],
+    K = KB D the padded K (the inverse of kt_rows, then of group_rows), byte address by byte
+    address."""
+    flat = np.asarray(data, np.uint8).reshape(-1)
+    R = grp_r(fmt, wg)
+    KB = K // D
+    P = wg * D
+    out = np.zeros((N, row_bytes(K, fmt)), np.uint8)
+    for n in range(N):
+        g, j = divmod(n, R)
+        lane = j if fmt == "int8" else j // 2
+        for c in range(KB):
+            m, h0 = kt_group_chunk(g, c, KB)
+            h = chunk_fold((at // P) + m, wg) if at is not None else 0
+            base = m * P + (lane ^ h) * D + h0
+            nb = D // 2 if c == KB - 1 else D                 # the tail's upper half: zeros
+            src = flat[base:base + nb]
+            if fmt == "int8":
+                out[n, c * D:c * D + nb] = src
+            else:
+                nib = (src >> (4 * (j % 2))) & 15               # element c D + i in lane byte i
+                e = c * D + np.arange(nb)
+                np.bitwise_or.at(out[n], e // 2, (nib << (4 * (e % 2))).astype(np.uint8))
+    return out
+
+
+def kt_scales(areas, fmt: str, K: int, wg: int, rsc: bool = False) -> np.ndarray:
+    """Grouped scale areas -> MM KT's (`opentpu/quant.py:861-880`): the odd groups' block entries
+    in chunk order (the tail block's first); a 4-bit tail word's bits 8..19 (sub-blocks 0, 1)
+    also into bits 20..31."""
+    areas = np.array(areas, np.uint8)
+    if rsc or areas.shape[0] < 2:
+        return areas
+    if fmt == "nvfp4":
+        raise ValueError("kt_scales: nvfp4 has no K tail")
+    R = grp_r(fmt, wg)
+    KB = K // D
+    sb, p = SCALE_DATA[fmt], swp(fmt, R)
+    for g in range(1, areas.shape[0], 2):
+        old = areas[g].copy()
+        for j in range(R):
+            for k in range(KB):
+                src = p + ((KB - 1 if k == 0 else k - 1) * R + j) * sb
+                dst = p + (k * R + j) * sb
+                areas[g, dst:dst + sb] = old[src:src + sb]
+            if fmt in ("int4", "fp4"):
+                at = p + j * sb                                  # the tail entry, now first
+                w = int(areas[g, at:at + 4].view("<u4")[0])
+                w = (w & 0xFFFFF) | (((w >> 8) & 0xFFF) << 20)
+                areas[g, at:at + 4] = np.array([w], "<u4").view(np.uint8)
+    return areas
+
+
+def ungroup_kt_scales(areas, N: int, K: int, fmt: str, wg: int, rsc: bool = False) -> np.ndarray:
+    """MM KT's scale areas -> natural scale rows: the odd groups' entries back in block order
+    (the 4-bit tail word kept as stored: its sub-block 2 and 3 multipliers meet zeros)."""
+    a = np.array(areas, np.uint8)
+    if not rsc and a.shape[0] >= 2:
+        R = grp_r(fmt, wg)
+        KB = K // D
+        sb, p = SCALE_DATA[fmt], swp(fmt, R)
+        for g in range(1, a.shape[0], 2):
+            old = a[g].copy()
+            for j in range(R):
+                for k in range(KB):
+                    src = p + ((0 if k == KB - 1 else k + 1) * R + j) * sb
+                    dst = p + (k * R + j) * sb
+                    a[g, dst:dst + sb] = old[src:src + sb]
+    return ungroup_scales(a, N, K, fmt, wg, rsc)
 
 
 def _scale_map(N: int, K: int, fmt: str, wg: int, rsc: bool):

@@ -2,8 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
-MM restated from `opentpu/isasim.py:749-910` (natural row layout, rows of one: WG = 1, no PAIR /
-KT / SPL) and `docs/isa.md:226-305`:
+MM restated from `opentpu/isasim.py:749-910` (natural row layout, rows of one: WG = 1, no PAIR
+or KT; SPL below) and `docs/isa.md:226-305`:
 
     for each output (j, n):  acc = sum over blocks k, groups g of B * c
         c  = sum_{i in g} q[j, i] * w[n, i]            exact; |c| < 2^19 (int8), 2^16 (4-bit)
@@ -12,10 +12,21 @@ KT / SPL) and `docs/isa.md:226-305`:
     y = mul(mul(i2f(acc), Sw[n]), mul(Sa[j], 2^-W))     three FTZ/RNE products
     ACC: y = add(old, y);  ASCALE: y = add(mul(old, alpha[j]), y);  RMAX: row max of the y.
 
+SPL (split terms, `opentpu/isasim.py:757-770`, `:849-852`, `:872-873`; `docs/isa.md:414-441`):
+one MM over a split operand's terms, one block (D = 128) of int8 RSC weights a part:
+
+    KB 3: acc = sum_g [ c(hi, w_hi) << (16 - da)  +  c(lo, w_hi) << (8 - da)  +  c(hi, w_lo) << (8 - da) ]
+    KB 2: acc = sum_g [ c(hi, w_hi) << (16 - da)  +  c(hi, w_lo) << (8 - da) ]
+    (a term whose shift is negative adds nothing); y = (i2f(acc) * Sw) * (Sa_hi * 2^-16)
+
 ARGMAX / greedy restated from `opentpu/isasim.py:1141-1152`, `opentpu/fp32.py:110-121`,
 `opentpu/llm/generate.py:251-286`: the first index whose total-order key is largest.
 
-Pinning (tests/test_oracle_mm.py): a scalar Python-int model written from docs/isa.md (the
+Pinning (tests/test_oracle_mm.py):
+SPL: a scalar Python-int model of the docs/isa.md pseudo-code with the advance table (KB 3:
+ACT hi, lo, hi against rows hi, hi, lo; KB 2: hi, hi against hi, lo), and the closed form at
+zero offsets acc = 2^16 hi.w_hi + 2^8 (lo.w_hi + hi.w_lo).
+MM: a scalar Python-int model written from docs/isa.md (the
 shape of the reference's `tests/test_mx.py:131-151` ref_mm) on the reference's CASES and
 seeds; the reference's integer model with asserted drops (`tests/test_isa.py:85-118`); closed
 forms (UNIT MM = plain integer dot; RSC + ROW activations: acc = 2^W * sum q w); the ARGMAX
@@ -83,6 +94,29 @@ def mm(q, Sa, da, rows, srows, fmt: str, K: int, *, flags: int = 0, k0: int = 0,
     if flags & RMAX:
         return y, rowmax(y)
     return y
+
+
+def mm_spl(q, Sa, da, w_hi, w_lo, Sw, nterms: int, *, old=None):
+    """MM SPL's outputs [M, N]: q int8 [M, 128] (KB 2) or [M, 256] (KB 3: hi, then lo, as QACT HL
+    writes them), Sa [M] (hi's), da uint8 [M, 4] (the hi part's offsets; lo shares them), w_hi /
+    w_lo int8 [N, 128] (the weights' hi and lo rows), Sw [N] (hi's).  old: ACC."""
+    if nterms not in (2, 3):
+        raise ValueError("SPL takes 2 or 3 terms")
+    q = np.asarray(q, np.int8)
+    M = q.shape[0]
+    hi = q[:, :D]
+    lo = q[:, D:2 * D] if nterms == 3 else None
+    wh = np.asarray(w_hi, np.uint8)[:, :D].view(np.int8)
+    wl = np.asarray(w_lo, np.uint8)[:, :D].view(np.int8)
+    terms = [(hi, wh, 0), (lo, wh, 8), (hi, wl, 8)] if nterms == 3 else [(hi, wh, 0), (hi, wl, 8)]
+    da = np.asarray(da, np.int64)[:, :NSUB]                           # [M, 4]
+    acc = np.zeros((M, wh.shape[0]), np.int64)
+    for a, w, e in terms:
+        c = group_sums(a, w, D // NSUB)                               # [M, N, 4]
+        sh = WINDOW["int8"] - (da[:, None, :] + e)
+        acc += np.where(sh >= 0, c << np.maximum(sh, 0), 0).sum(axis=2)
+    y = epilogue(acc, np.asarray(Sw, np.float32), Sa, "int8")
+    return F.add(np.asarray(old, np.float32), y) if old is not None else y
 
 
 def rowmax(y) -> np.ndarray:

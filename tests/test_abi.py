@@ -14,7 +14,7 @@ def declared():
     src = open(os.path.join(ROOT, "include", "otpu.h")).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     out = {}
-    for m in re.finditer(r"(?:int|const char\*)\s+(otpu_\w+)\s*\(([^)]*)\)\s*;", src):
+    for m in re.finditer(r"(?:int64_t|int|const char\*)\s+(otpu_\w+)\s*\(([^)]*)\)\s*;", src):
         args = [a for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
         out[m.group(1)] = len(args)
     return out
@@ -23,8 +23,10 @@ def declared():
 def test_header_declares_the_entry_points():
     d = declared()
     for name in ("otpu_qact", "otpu_mm", "otpu_mm_acc", "otpu_mm_batched", "otpu_lm_head_argmax",
-                 "otpu_argmax", "otpu_pack_int8", "otpu_pack_x4", "otpu_last_error", "otpu_version"):
+                 "otpu_argmax", "otpu_pack_int8", "otpu_pack_x4", "otpu_last_error", "otpu_version",
+                 "otpu_sample_work_bytes", "otpu_lda", "otpu_mm_spl"):
         assert name in d
+    assert set(d) == set(_lib.SIGNATURES), set(d) ^ set(_lib.SIGNATURES)
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="libotpu_amd.so not built")

@@ -49,7 +49,7 @@ def test_qact_ranges(X, width, mul):
     S = torch.empty((R * M,), dtype=torch.float32, device="cuda")
     d = torch.empty((M, K // 32), dtype=torch.uint8, device="cuda")
     X.call("otpu_qact_ranges", X.ptr(ad), X.ptr(ad[:, K:]) if mul else None, M, K, 2 * K, width, 32, 0,
-           X.ptr(q), K, X.ptr(S), X.ptr(d), K // 32, X.stream())
+           None, None, X.ptr(q), K, X.ptr(S), X.ptr(d), K // 32, X.stream())
     src = F.mul(x, u) if mul else x
     qh, Sh, dh = q.cpu().numpy(), S.cpu().numpy().reshape(R, M), d.cpu().numpy()
     for r in range(R):
@@ -141,8 +141,8 @@ def test_mm_qin(X, fmt, K, width, nsum, mul):
     xd, wd, sd = d(xs), d(rows), d(srows)
     xmd = d(xm) if mul else None
     out = torch.full((R, N), 7.0, dtype=torch.float32, device="cuda")
-    X.call("otpu_mm_qin", X.ptr(xd), X.ptr(xmd), nsum, K, K, width, X.ptr(wd), rows.shape[1], X.ptr(sd),
-           srows.shape[1], N, X.FMT[fmt], 0, 0, X.ptr(out), N, N, X.stream())
+    X.call("otpu_mm_qin", X.ptr(xd), X.ptr(xmd), None, None, nsum, K, K, width, X.ptr(wd), rows.shape[1],
+           X.ptr(sd), srows.shape[1], N, X.FMT[fmt], 0, 0, X.ptr(out), N, N, X.stream())
     got = out.cpu().numpy()
     for r in range(R):
         q, Sa, da = F.quantize_mx(src[:, r * width:(r + 1) * width], 32)
@@ -167,8 +167,8 @@ def test_mm_qin_fold(X, fmt, K, N):
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     gd, ud, wd, sd = d(g), d(u), d(rows), d(srows)
     out = torch.full((1, N), 7.0, dtype=torch.float32, device="cuda")
-    X.call("otpu_mm_qin_fold", X.ptr(gd), X.ptr(ud), K, X.ptr(wd), rows.shape[1], X.ptr(sd), srows.shape[1], N,
-           X.FMT[fmt], 0, 0, X.ptr(out), X.stream())
+    X.call("otpu_mm_qin_fold", X.ptr(gd), X.ptr(ud), None, None, K, X.ptr(wd), rows.shape[1], X.ptr(sd),
+           srows.shape[1], N, X.FMT[fmt], 0, 0, X.ptr(out), X.stream())
     assert same_bits(out.cpu().numpy(), want)
 
 
@@ -179,7 +179,7 @@ def test_mm_qin_fold_refusals(X):
                  (1024, X.FMT["int4"], X.RSC)]:
         K, fmt, flags = args
         with pytest.raises(OtpuError):
-            X.call("otpu_mm_qin_fold", p, p, K, p, 512, p, 40, 8, fmt, flags, 0, p, X.stream())
+            X.call("otpu_mm_qin_fold", p, p, None, None, K, p, 512, p, 40, 8, fmt, flags, 0, p, X.stream())
 
 
 def test_acc_rows(X):
@@ -239,6 +239,37 @@ def test_chain_layers_small(X):
     yd = torch.empty((1, 256), dtype=torch.float32, device="cuda")
     ch.layer_folded(1, torch.from_numpy(x).cuda(), yd)
     assert same_bits(yd.cpu().numpy(), CH.layer(x, host[1], "int4", 512, 768)[0])
+
+
+def test_chain_with_norms(X):
+    """Per-layer RMSNorm factors riding in the qkv and gate / up QACTs (CSCALE gamma, RSCALE r):
+    every path (fused, folded, partial rows, unfused, graph replay) against the oracle's layers
+    with the same factors, bit for bit."""
+    import torch
+    from opentpu_amd.chain import DecodeChain, Shape
+    sh = Shape(hidden=256, q_dim=512, kv_dim=256, F=768, layers=3)
+    say("chain with norms: pack")
+    base = DecodeChain.synthetic(sh, "int4", seed0=9, std=0.05)
+    rng = np.random.default_rng(8)
+    norms = [(rng.uniform(0.5, 2.0, 256).astype(np.float32), rng.uniform(0.5, 2.0, 256).astype(np.float32))
+             for _ in range(sh.layers)]
+    ch = DecodeChain(base.layers, sh, "int4", True, norms)
+    r = rng.uniform(0.5, 3.0, (sh.layers, 2)).astype(np.float32)
+    ch.rnorm.copy_(torch.from_numpy(r).cuda())
+    host = _host_layers(ch)
+    onorms = [(norms[l][0], norms[l][1], r[l, 0:1], r[l, 1:2]) for l in range(sh.layers)]
+    x = rng.standard_normal((1, 256)).astype(np.float32)
+    want = CH.step(x, host, "int4", 512, 768, onorms)
+    assert not same_bits(want, CH.step(x, host, "int4", 512, 768))
+    for fused, fold in ((True, True), (True, False), (False, True)):
+        ch.fused, ch.fold = fused, fold
+        say("chain with norms", fused, fold)
+        assert same_bits(ch.step(x).cpu().numpy(), want), (fused, fold)
+    ch.fused, ch.fold = True, True
+    ch.capture()
+    for i in range(2):
+        assert same_bits(ch.replay(x).cpu().numpy(), want), f"replay {i}"
+        torch.cuda.synchronize()
 
 
 def test_chain_c4_full_and_graph(X):

@@ -97,6 +97,36 @@ def test_mm_over_a_grouped_image(X, fmt):
     assert same_bits(got, want)
 
 
+@pytest.mark.parametrize("fmt", ["int8", "int4", "fp4"])
+@pytest.mark.parametrize("wg,hashed", [(2, False), (8, True), (16, False)])
+@pytest.mark.parametrize("groups,KB", [(1, 1), (2, 5), (3, 2), (4, 23)])
+def test_ungroup_kt_pairs(X, fmt, wg, hashed, groups, KB):
+    """An image in MM KT's pairs (the oracle's kt_rows / kt_scales of a grouped image whose K ends
+    in the first half of its last block) comes back as the padded natural rows byte for byte; its
+    scale rows equal the natural ones wherever they meet data; the MM over it is the padded MM
+    bit for bit (the reference's tests/test_kt.py:94-113 property)."""
+    from opentpu_amd import mxu, quant as QA
+    from test_oracle_kt import kt_operand
+    say(f"ungroup kt fmt={fmt} wg={wg} hashed={hashed} groups={groups} KB={KB}")
+    rng = np.random.default_rng(wg * 10 + groups * 100 + KB)
+    R = G.grp_r(fmt, wg)
+    N = groups * R - (3 if groups == 3 else 0)
+    K = KB * D
+    rows, srows = kt_operand(rng, fmt, N, KB)
+    g = G.kt_rows(G.group_rows(rows, N, K, fmt, wg), wg)
+    a = G.kt_scales(G.group_scales(srows, N, K, fmt, wg), fmt, K, wg)
+    at = 11 * wg * D if hashed else None
+    if hashed:
+        g = G.hash_rows(g, at, wg)
+    r2, s2 = QA.ungrouped(g, a, N, K, wg, fmt, at=at, kt=True)
+    assert np.array_equal(r2, rows)
+    assert np.array_equal(s2, G.ungroup_kt_scales(a, N, K, fmt, wg))
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    x[:, K - D // 2:] = 0                                         # K ends in the tail block's first half
+    q, S, d = F.quantize_mx(x, 32)
+    assert same_bits(mxu.mm(q, S, d, r2, s2, fmt, K), MM.mm(q, S, d, rows, srows, fmt, K))
+
+
 def test_ungroup_lm_head_shape(X):
     """An LM-head-sized int4 image (N 8192 of K 2560, WG 8, hashed): byte for byte."""
     from opentpu_amd import quant as QA
@@ -120,14 +150,18 @@ def test_ungroup_refusals(X):
     out = torch.zeros((N, K), dtype=torch.uint8, device="cuda")
     s = torch.cuda.current_stream().cuda_stream
     with pytest.raises(X.OtpuError, match="power of two"):
-        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 3, 0, -1, X.ptr(out), K, s)
+        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 3, 0, 0, -1, X.ptr(out), K, s)
     with pytest.raises(X.OtpuError, match="not a multiple"):
-        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 8, 0, 128, X.ptr(out), K, s)
+        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 8, 0, 0, 128, X.ptr(out), K, s)
     with pytest.raises(X.OtpuError, match="need"):
-        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 8, 0, -1, X.ptr(out), 128, s)
+        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 8, 0, 0, -1, X.ptr(out), 128, s)
     with pytest.raises(X.OtpuError):
-        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 8, 7, -1, X.ptr(out), K, s)
+        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 8, 7, 0, -1, X.ptr(out), K, s)
     with pytest.raises(X.OtpuError, match="NVFP4"):
-        X.call("otpu_ungroup_scales", X.ptr(d), N, K, 8, 3, 1, X.ptr(out), K, s)
+        X.call("otpu_ungroup_scales", X.ptr(d), N, K, 8, 3, 1, 0, X.ptr(out), K, s)
+    with pytest.raises(X.OtpuError, match="KT"):
+        X.call("otpu_ungroup_rows", X.ptr(d), N, K, 1, 0, 1, -1, X.ptr(out), K, s)
+    with pytest.raises(X.OtpuError, match="KT"):
+        X.call("otpu_ungroup_scales", X.ptr(d), N, K, 8, 3, 0, 1, X.ptr(out), K, s)
     with pytest.raises(ValueError, match="image"):
         QA.ungroup_rows(d[:, :100], N, K, 8, "int8")

@@ -274,15 +274,18 @@ def test_batched_is_independent_mms(ops):
         assert same_bits(got[b], want[b])
 
 
-@pytest.mark.parametrize("fmt,rsc", [("int8", True), ("int8", False), ("int4", False), ("fp4", False)])
-def test_gemv_row_blocking_paths(ops, fmt, rsc):
+@pytest.mark.parametrize("fmt,rsc,K", [("int8", True, 1024), ("int8", False, 1024), ("int4", False, 1024),
+                                       ("fp4", False, 1024), ("int4", False, 2048), ("fp4", False, 2048),
+                                       ("nvfp4", False, 2048)])
+def test_gemv_row_blocking_paths(ops, fmt, rsc, K):
     """One launch of 32 problems (a grid over every CU: 8 rows a team) and the same problems
-    one launch each (a small grid: 4 rows a team), both against the C oracle."""
+    one launch each (a small grid: 4 rows a team), both against the C oracle.  K 2048 4-bit is
+    the timed headline's kernel: a team of 64 lanes, one piece a lane, 8 rows a team."""
     import torch
     _, _, mxu = ops
     from opentpu_amd import _lib as X
-    rng = np.random.default_rng(31 + len(fmt) + rsc)
-    B, N, K = 32, 512, 1024
+    rng = np.random.default_rng(31 + len(fmt) + rsc + K)
+    B, N = 32, 512
     qs, Sas, das, rs, ss, want = [], [], [], [], [], []
     flags = MM.RSC if rsc else 0
     for b in range(B):
@@ -291,7 +294,7 @@ def test_gemv_row_blocking_paths(ops, fmt, rsc):
         if fmt == "int8":
             r, sr = Q.pack_rsc(W) if rsc else Q.pack_int8x(W)
         else:
-            r, sr = Q.pack_x4(W, fmt)
+            r, sr = Q.quantize_mxu(W, fmt)
         q, Sa, da = F.quantize_mx(x, 32)
         qs.append(q); Sas.append(Sa); das.append(da); rs.append(r); ss.append(sr)
         want.append(OC.mm(q, Sa, da, r, sr, fmt, K, flags=flags))
@@ -310,6 +313,42 @@ def test_gemv_row_blocking_paths(ops, fmt, rsc):
         assert same_bits(got[b], want[b])
         one = mxu.mm(qs[b], Sas[b], das[b], rs[b], ss[b], fmt, K, rsc=rsc)
         assert same_bits(one, want[b])
+
+
+def test_headline_batched_c2_full_size(ops):
+    """The bench's timed headline launch itself: 80 independent c2 GEMVs (int4x N=6144 K=2048,
+    weights N(0, 0.02) packed on the GPU, MX activations of N(0, 1) rows) in one otpu_mm_batched
+    (a team of 64 lanes, one piece a lane, 8 rows a team), every output bit against the C
+    oracle."""
+    import torch
+    _, quant, _ = ops
+    from opentpu_amd import _lib as X
+    from opentpu_amd import fp32 as GF
+    B, N, K = 80, 6144, 2048
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    rows = torch.empty((B, N, 1024), dtype=torch.uint8, device="cuda")
+    srows = torch.empty((B, N, 72), dtype=torch.uint8, device="cuda")
+    say("headline c2 x 80: pack")
+    for b in range(B):
+        W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+        r, sr = quant.quantize_mxu(W, "int4")
+        rows[b].copy_(r)
+        srows[b].copy_(sr)
+    x = torch.randn((B, K), generator=gen, device="cuda")
+    q, Sa, da = GF.quantize_mx(x, 32)
+    out = torch.empty((B, N), dtype=torch.float32, device="cuda")
+    say("headline c2 x 80: run")
+    X.call("otpu_mm_batched", B, X.ptr(q), K, K, X.ptr(Sa), 1, X.ptr(da), K // 32, K // 32, 1, K, X.ptr(rows), 1024,
+           N * 1024, X.ptr(srows), 72, N * 72, N, X.FMT["int4"], 0, 0, X.ptr(out), N, N, X.stream())
+    got = out.cpu().numpy()
+    qh, Sh, dh = q.cpu().numpy(), Sa.cpu().numpy(), da.cpu().numpy()
+    q0, S0, d0 = F.quantize_mx(x.cpu().numpy(), 32)
+    assert np.array_equal(qh, q0) and same_bits(Sh, S0) and np.array_equal(dh, d0)
+    rh, sh = rows.cpu().numpy(), srows.cpu().numpy()
+    say("headline c2 x 80: oracle")
+    for b in range(B):
+        want = OC.mm(qh[b:b + 1], Sh[b:b + 1], dh[b:b + 1], rh[b], sh[b], "int4", K)
+        assert same_bits(got[b:b + 1], want), f"problem {b}"
 
 
 GEMM_CASES = [  # M, N, K, weights (rsc | int8x | unit), activations (row | mx | wide), k0

@@ -33,13 +33,39 @@ def S():
 
 
 @pytest.mark.parametrize("i", range(10))
-def test_picks_match_the_reference(S, i):
+@pytest.mark.parametrize("nu", [4096, 1, 16, 17])
+def test_picks_match_the_reference(S, i, nu):
+    """Every uniform of a golden case (the pick's wave loop), and the first 1, 16 and 17 (a decode
+    step's one uniform: the pick's path for at most 16 uniforms, and the boundary after it)."""
     g = np.load(GOLD)
     T, k, P, R, cap, V, masked = g["cases"][i]
-    say(f"sampler golden case {i}: T={T} k={k} P={P} R={R} cap={cap} V={int(V)} masked={int(masked)}")
+    say(f"sampler golden case {i}: T={T} k={k} P={P} R={R} cap={cap} V={int(V)} masked={int(masked)} nu={nu}")
     samp = S.Sampling(T, int(k), P, R)
-    got = S.pick(g[f"s{i}_logits"], samp, g[f"s{i}_ctx"].tolist(), g[f"s{i}_u"], cap or None)
-    assert np.array_equal(got, g[f"s{i}_ids"])
+    u = g[f"s{i}_u"][:nu]
+    got = S.pick(g[f"s{i}_logits"], samp, g[f"s{i}_ctx"].tolist(), u, cap or None)
+    assert np.array_equal(got, g[f"s{i}_ids"][:nu])
+
+
+@pytest.mark.parametrize("nu,offset", [(1, 0), (16, 0), (17, 0), (1, 1), (5, 3)])
+def test_pick_few_uniforms_and_misaligned_logits(S, nu, offset):
+    """V 262144 with masked blocks, few uniforms (the decode step's path, up to 16), and logits
+    that start 4 or 12 bytes past a 16-byte boundary (the scalar-load path), against the oracle."""
+    import torch
+    V = 262144
+    rng = np.random.default_rng(nu + 10 * offset)
+    lg = (rng.standard_normal(V) * 3).astype(np.float32)
+    for b in rng.choice(V // 64, 40, replace=False):
+        lg[64 * b:64 * (b + 1)] = -np.inf
+    ctx = rng.integers(0, V, 30).tolist()
+    samp, osamp = S.Sampling(0.8, 50, 0.9, 1.1), SP.Sampling(0.8, 50, 0.9, 1.1)
+    u = rng.random(nu).astype(np.float32)
+    say(f"sampler few uniforms nu={nu} offset={offset}")
+    buf = torch.zeros(V + 8, dtype=torch.float32, device="cuda")
+    buf[offset:offset + V] = torch.from_numpy(lg).cuda()
+    sm = S.Sampler(V, samp, ctx)
+    ids = sm.pick_device(buf[offset:offset + V], torch.from_numpy(u).cuda())
+    sm.check()
+    assert np.array_equal(ids.cpu().numpy(), SP.pick(lg, osamp, ctx, u))
 
 
 @pytest.mark.parametrize("V,T,k,P,R,cap,masked", [
