@@ -27,16 +27,32 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build(verbose: bool = True) -> str:
-    """Compile every source to an object in parallel (one hipcc per file), then link."""
+def _stale(src: str, obj: str) -> bool:
+    """obj is older than src or than any header under csrc/ or include/."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [src] + glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(HERE, "..", "include", "*.h"))
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def build(verbose: bool = True, incremental: bool = False) -> str:
+    """Compile every source to an object in parallel (one hipcc per file), then link.
+    incremental: keep the objects in csrc/_build and recompile only those older than their
+    source or a header (a developer's loop; the default compiles everything)."""
     import tempfile
     from concurrent.futures import ThreadPoolExecutor
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     inc = ["-I", os.path.join(HERE, "..", "include")]
     cflags = [f for f in FLAGS if f != "-shared"]
+    keep = os.path.join(CSRC, "_build")
+    if incremental:
+        os.makedirs(keep, exist_ok=True)
     with tempfile.TemporaryDirectory(prefix="otpu_build_") as tmpd:
         def compile_one(src):
-            obj = os.path.join(tmpd, os.path.basename(src) + ".o")
+            obj = os.path.join(keep if incremental else tmpd, os.path.basename(src) + ".o")
+            if incremental and not _stale(src, obj):
+                return obj, subprocess.CompletedProcess([], 0, "", "")
             cmd = [hipcc, *cflags, *inc, "-c", src, "-o", obj]
             if verbose:
                 print(" ".join(cmd), flush=True)
@@ -62,4 +78,4 @@ def build(verbose: bool = True) -> str:
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv)

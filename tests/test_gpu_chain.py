@@ -325,3 +325,28 @@ def test_chain_c4_full_and_graph(X):
         assert same_bits(got, exp), f"replay {i}"
         torch.cuda.synchronize()
         ch.qkv.fill_(float(i))                     # eager work between replays
+
+
+def test_chain_c4_layers_against_the_float64_emulation(X):
+    """The c4 layers 0, 13 and 27 on live N(0, 1) inputs, every linear of the GPU's fused, folded
+    layer against the float64 layer with the quantization points (oracle/chain.py
+    emulated_layer: the reference's emulated_logits structure) within EMU_TOL of the linear's
+    largest output: quantization error and machine rounding apart from kernel bugs."""
+    import torch
+    from opentpu_amd.chain import DecodeChain, Shape
+    from test_oracle_chain import EMU_TOL
+    say("chain c4 emulation: pack")
+    ch = DecodeChain.synthetic(Shape(), "int4", seed0=100)
+    rng = np.random.default_rng(13)
+    for l in (0, 13, 27):
+        host = {k: (r.cpu().numpy(), s.cpu().numpy()) for k, (r, s) in ch.layers[l].items()}
+        x = rng.standard_normal((1, 1024)).astype(np.float32)
+        yd = torch.empty((1, 1024), dtype=torch.float32, device="cuda")
+        say("chain c4 emulation: layer", l)
+        ch.layer_folded(l, torch.from_numpy(x).cuda(), yd)
+        ye, me = CH.emulated_layer(x, host, "int4")
+        got = {"qkv": ch.qkv.cpu().numpy(), "o": ch.o.cpu().numpy(), "gu": ch.gu.cpu().numpy(),
+               "down": yd.cpu().numpy()}
+        for k, g in got.items():
+            err = np.abs(g.astype(np.float64) - me[k]).max()
+            assert err <= EMU_TOL * np.abs(me[k]).max(), (l, k, err / np.abs(me[k]).max())

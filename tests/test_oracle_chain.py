@@ -93,3 +93,36 @@ def test_layer_small():
     assert same_bits(mid["h"], F.mul(mid["gu"][:, :Fd], mid["gu"][:, Fd:]))
     assert same_bits(y, CH.ranges_dot(mid["h"], wts["down"], "int4", 256))
     assert np.any(y != 0)
+
+
+EMU_TOL = 1e-5       # of the largest output of each linear: the machine's fp32 chain vs float64
+
+
+def test_emulated_layer_separates_quantization_from_rounding():
+    """The float64 layer with the quantization points (emulated_layer, the structure of the
+    reference's emulated_logits) is within EMU_TOL of the machine's fp32 layer at every linear;
+    the same product without the quantization points, and the machine's layer with a wrong
+    F-chunking of the down input, are hundreds of times further."""
+    from oracle import emulate as EM
+    rng = np.random.default_rng(1)
+    h, qd, kv, Fd = 256, 512, 256, 768
+
+    def pack(n, k):
+        return Q.quantize_mxu((rng.standard_normal((n, k)) * 0.05).astype(np.float32), "int4")
+    wts = {"qkv": pack(qd + 2 * kv, h), "o": pack(h, qd), "gu": pack(2 * Fd, h), "down": pack(h, Fd)}
+    for _ in range(3):
+        x = rng.standard_normal((1, h)).astype(np.float32)
+        y, mid = CH.layer(x, wts, "int4", qd, Fd)
+        ye, me = CH.emulated_layer(x, wts, "int4", qd, Fd)
+        for k in ("qkv", "o", "gu", "down"):
+            assert np.abs(np.asarray(mid[k], np.float64) - me[k]).max() <= EMU_TOL * np.abs(me[k]).max(), k
+
+        def plain(xx, w):
+            return xx @ EM.fake_w(w[0], w[1], "int4", xx.shape[1])[0].T
+        xf = x.astype(np.float64)
+        qkv = plain(xf, wts["qkv"])
+        gu = plain(plain(qkv[:, :qd], wts["o"]), wts["gu"])
+        yp = plain(gu[:, :Fd] * gu[:, Fd:], wts["down"])
+        assert np.abs(yp - ye).max() > 100 * EMU_TOL * np.abs(ye).max()
+        yb = CH.ranges_dot(mid["h"], wts["down"], "int4", 768)
+        assert np.abs(yb - ye).max() > 100 * EMU_TOL * np.abs(ye).max()
