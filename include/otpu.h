@@ -264,6 +264,17 @@ int otpu_sample(const float* logits, int V, const float* pa, const float* pb, do
                 float itemp, float top_p, const float* u, int nu, void* work, int32_t* ids,
                 int32_t* status, otpu_stream_t stream);
 
+/* otpu_sample with no work argument and no allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops that
+ * forbid it).  The work area is the library's own static device array (1,066,496 bytes on each
+ * device the library runs on, held until the process ends), looked up once per device with that
+ * device current; so V is at most 262144 (larger: OTPU_EINVAL, use otpu_sample).  The candidate
+ * values and ids of the last call stay in that array.  Calls that overlap on one device (two
+ * streams, two threads) race on the one array: serialize them. */
+int otpu_sample_static(const float* logits, int V, const float* pa, const float* pb, double softcap,
+                       int k, float itemp, float top_p, const float* u, int nu, int32_t* ids,
+                       int32_t* status, otpu_stream_t stream);
+
 /* The reference's float64 emulation (opentpu/quant.py:895-1067), for checking model code
  * against the operator:
  *   otpu_fake_act: quant.fake_act of x [M, K] fp32 in ranges of n columns (K a multiple of n),

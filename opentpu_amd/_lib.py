@@ -47,6 +47,7 @@ SIGNATURES = {
     "otpu_import_nvfp4": ([_P, _L, _P, _L, _F, _I, _I, _P, _L, _P, _L, _P, _P], _I),
     "otpu_sample_work_bytes": ([_I], _L),
     "otpu_sample": ([_P, _I, _P, _P, _D, _I, _F, _F, _P, _I, _P, _P, _P, _P], _I),
+    "otpu_sample_static": ([_P, _I, _P, _P, _D, _I, _F, _F, _P, _I, _P, _P, _P], _I),
     "otpu_fake_act": ([_P, _I, _I, _L, _I, _I, _I, _P, _L, _P, _L, _P], _I),
     "otpu_dequant": ([_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P], _I),
     "otpu_mx_matmul": ([_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P, _L, _P], _I),

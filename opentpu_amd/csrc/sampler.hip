@@ -26,6 +26,7 @@
 // (m >= 1) all take the first position among the taken ones and the -inf ones, with value
 // -inf; that is applied to the sorted list (only then is the first -inf position looked up).
 #include <climits>
+#include <mutex>
 
 #include "otpu_common.h"
 
@@ -462,14 +463,44 @@ __global__ __launch_bounds__(SNT) void sample_pick(SampleArgs a) {
 using namespace otpu;
 
 // work area: vs [64] fp32, si [64] int32, lg [nb x 64], bm [nb], sbm [ceil(nb / 16)]
-extern "C" int64_t otpu_sample_work_bytes(int V) {
-    const int64_t nb = ((int64_t)V + SBLK - 1) / SBLK;
-    return 4 * (2 * SKMAX + nb * SBLK + nb + (nb + SGRP - 1) / SGRP);
+constexpr int64_t sample_work_bytes(int64_t V) {
+    return 4 * (2 * SKMAX + (V + SBLK - 1) / SBLK * SBLK + (V + SBLK - 1) / SBLK
+                + ((V + SBLK - 1) / SBLK + SGRP - 1) / SGRP);
 }
 
-extern "C" int otpu_sample(const float* logits, int V, const float* pa, const float* pb, double softcap, int k,
-                           float itemp, float top_p, const float* u, int nu, void* work, int32_t* ids,
-                           int32_t* status, otpu_stream_t stream) {
+extern "C" int64_t otpu_sample_work_bytes(int V) { return sample_work_bytes(V); }
+
+// otpu_sample_static's work area: one per device, in the library's own device memory, for
+// vocabularies of at most SAMPLE_STATIC_VMAX (1,066,496 bytes); every call overwrites all of
+// the area it reads before reading it, so nothing is cleared between calls
+constexpr int SAMPLE_STATIC_VMAX = 262144;
+constexpr int SCRATCH_DEVICES = 64;
+static __device__ __align__(256) uint8_t scratch[sample_work_bytes(SAMPLE_STATIC_VMAX)];
+static void* scratch_ptr[SCRATCH_DEVICES];
+static std::mutex scratch_mu;
+
+// the current device's address of `scratch`: the array's name is a host-side stand-in, so its
+// device address is looked up once per device (hipGetSymbolAddress with that device current)
+static int scratch_of_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return otpu_fail(OTPU_ENODEV, "sample_static: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= SCRATCH_DEVICES) return otpu_fail(OTPU_ENODEV, "sample_static: device %d", dev);
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return otpu_fail(OTPU_ELAUNCH, "sample_static: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return OTPU_OK;
+}
+
+static int sample_launch(const float* logits, int V, const float* pa, const float* pb, double softcap, int k,
+                         float itemp, float top_p, const float* u, int nu, void* work, int32_t* ids,
+                         int32_t* status, otpu_stream_t stream) {
     if (V < 1 || (int64_t)V > (int64_t)NB_MAX * SBLK)
         return otpu_fail(OTPU_EINVAL, "sample: vocabulary %d (1 .. %lld)", V, (long long)NB_MAX * SBLK);
     if (k < 1 || k > SKMAX) return otpu_fail(OTPU_EINVAL, "sample: top_k %d (1 .. %d)", k, SKMAX);
@@ -509,4 +540,21 @@ extern "C" int otpu_sample(const float* logits, int V, const float* pa, const fl
     if (int rc = otpu_launch_check("sample_blocks")) return rc;
     sample_pick<<<1, SNT, 0, s>>>(a);
     return otpu_launch_check("sample_pick");
+}
+
+extern "C" int otpu_sample(const float* logits, int V, const float* pa, const float* pb, double softcap, int k,
+                           float itemp, float top_p, const float* u, int nu, void* work, int32_t* ids,
+                           int32_t* status, otpu_stream_t stream) {
+    return sample_launch(logits, V, pa, pb, softcap, k, itemp, top_p, u, nu, work, ids, status, stream);
+}
+
+extern "C" int otpu_sample_static(const float* logits, int V, const float* pa, const float* pb, double softcap,
+                                  int k, float itemp, float top_p, const float* u, int nu, int32_t* ids,
+                                  int32_t* status, otpu_stream_t stream) {
+    if (V > SAMPLE_STATIC_VMAX)
+        return otpu_fail(OTPU_EINVAL, "sample_static: vocabulary %d above the static work area's %d (use otpu_sample)",
+                         V, SAMPLE_STATIC_VMAX);
+    void* work = nullptr;
+    if (int rc = scratch_of_current_device(&work)) return rc;
+    return sample_launch(logits, V, pa, pb, softcap, k, itemp, top_p, u, nu, work, ids, status, stream);
 }
