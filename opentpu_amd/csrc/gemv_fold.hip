@@ -28,7 +28,10 @@ __device__ __forceinline__ void fold_body(const MMArgs& a) {
     __shared__ __align__(16) uint32_t qs[QIN_KMAX / 4];
     __shared__ uint8_t ds[QIN_KMAX / 32];
     __shared__ float sa2s[FOLD_NRMAX];
-    constexpr int CPT = QIN_KMAX / 4 / 256;       // float4 chunks a thread holds at most
+    // float4 chunks a thread holds at most: K <= 32 L T (only the chunks that can exist are
+    // compiled: the code runs once per launch, from a cold instruction cache)
+    constexpr int CPT0 = (L * T * 8 + 255) / 256;
+    constexpr int CPT = CPT0 < QIN_KMAX / 4 / 256 ? CPT0 : QIN_KMAX / 4 / 256;
     constexpr int NT = 64 / T;                    // teams a wave
     constexpr int GPT = T / FOLD_PPR;             // ranges a team slot holds
     const int K = a.K, NC = K >> 2, W = window_of(FMT), P = a.P, NR = K / FOLD_C;
@@ -121,8 +124,9 @@ __device__ __forceinline__ void fold_body(const MMArgs& a) {
         }
         const float4 t = tv[k];
         const float sc = fmul(inv, pow2f(dg));
-        qs[c] = (uint32_t)(q8(fmul(t.x, sc)) & 0xFF) | ((uint32_t)(q8(fmul(t.y, sc)) & 0xFF) << 8)
-              | ((uint32_t)(q8(fmul(t.z, sc)) & 0xFF) << 16) | ((uint32_t)(q8(fmul(t.w, sc)) & 0xFF) << 24);
+        // t and sc are flushed: q8 of the IEEE product is q8 of fmul's
+        qs[c] = (uint32_t)(q8(t.x * sc) & 0xFF) | ((uint32_t)(q8(t.y * sc) & 0xFF) << 8)
+              | ((uint32_t)(q8(t.z * sc) & 0xFF) << 16) | ((uint32_t)(q8(t.w * sc) & 0xFF) << 24);
         if ((c & 7) == 0) ds[c >> 3] = (uint8_t)dg;
     }
     __syncthreads();

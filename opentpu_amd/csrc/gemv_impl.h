@@ -183,7 +183,12 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
     __shared__ __align__(16) uint32_t qs[QIN_KMAX / 4];
     __shared__ uint8_t ds[QIN_KMAX / 32];
     __shared__ uint32_t red[4];
-    constexpr int CPT = QIN_KMAX / 4 / 256;            // float4 chunks a thread holds at most
+    // float4 chunks a thread holds at most: the row has at most L T pieces of 16 (int8) or 32
+    // (4-bit) elements, so for the small rows of a chain only the chunks that can exist are
+    // compiled (the code runs once per launch, from a cold instruction cache)
+    constexpr int EPP = FMT == OTPU_INT8 ? 16 : 32;
+    constexpr int CPT0 = (L * T * EPP / 4 + 255) / 256;
+    constexpr int CPT = CPT0 < QIN_KMAX / 4 / 256 ? CPT0 : QIN_KMAX / 4 / 256;
     const int K = a.K, NC = K >> 2, W = window_of(FMT);
     const int tid = threadIdx.x;
     const float* x = a.xin + b * a.xin_bs;
@@ -285,8 +290,10 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
         }
         if (c < NC) {
             const float sc = fmul(inv, pow2f(dg));
-            qs[c] = (uint32_t)(q8(fmul(v[k].x, sc)) & 0xFF) | ((uint32_t)(q8(fmul(v[k].y, sc)) & 0xFF) << 8)
-                  | ((uint32_t)(q8(fmul(v[k].z, sc)) & 0xFF) << 16) | ((uint32_t)(q8(fmul(v[k].w, sc)) & 0xFF) << 24);
+            // v and sc are flushed: q8 of the IEEE product is q8 of fmul's (a denormal product
+            // rounds to 0 either way, NaN gives 0)
+            qs[c] = (uint32_t)(q8(v[k].x * sc) & 0xFF) | ((uint32_t)(q8(v[k].y * sc) & 0xFF) << 8)
+                  | ((uint32_t)(q8(v[k].z * sc) & 0xFF) << 16) | ((uint32_t)(q8(v[k].w * sc) & 0xFF) << 24);
             if ((c & 7) == 0) ds[c >> 3] = (uint8_t)dg;
         }
     }
@@ -456,6 +463,10 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a) {
                 // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw
                 // and the finished Sa * 2^-W need no operand flush
                 float y = fmul_f(fmul_f((float)tot, st.sw), sa2[ej]);
+                if constexpr (QIN) {                  // (no ACC / ASCALE / RMAX / LM head here)
+                    out[(int64_t)ej * a.ors + n] = y;
+                    return;
+                }
                 if (out) {
                     float* op = out + (int64_t)ej * a.ors + n;
                     if (a.flags & OTPU_ASCALE) y = fadd(fmul(*op, a.alpha[ej]), y);

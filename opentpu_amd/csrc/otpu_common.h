@@ -17,9 +17,13 @@ namespace otpu {
 __device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
 __device__ __forceinline__ float bitsf(uint32_t u) { return __uint_as_float(u); }
 
+// A denormal becomes the zero of its sign; everything else (NaN too) keeps its bits.  The
+// comparison runs on the subnormal grid (denormals are enabled in these builds), so |x| < 2^-126
+// holds exactly for the denormals and the zeros; three instructions (compare with the |.|
+// modifier, sign mask, select).  These kernels run their code once per launch from a cold
+// instruction cache, so the helpers' length is their latency.
 __device__ __forceinline__ float ftz(float x) {
-    uint32_t u = fbits(x);
-    return ((u & 0x7F800000u) == 0) ? bitsf(u & 0x80000000u) : x;
+    return __builtin_fabsf(x) < 0x1p-126f ? bitsf(fbits(x) & 0x80000000u) : x;
 }
 // an arithmetic result: flush a denormal, canonical NaN
 __device__ __forceinline__ float fin(float r) {
@@ -73,22 +77,25 @@ __device__ __forceinline__ float recip(float x) {
     uint32_t xb = fbits(x), mag = xb & 0x7FFFFFFFu, sign = xb & 0x80000000u;
     if (mag == 0) return 0.0f;
     if (mag >= 0x7E800000u) return bitsf(sign);
+    // Every value of the iteration is a normal float or zero (a in [1, 2), y in (0.47, 1], the
+    // residue 1 - a y a multiple of 2^-24 of at most 2^-22), so the FTZ operations of the
+    // definition are plain IEEE operations here: the same bits with no flush steps.
     float a = bitsf(0x3F800000u | (mag & 0x7FFFFFu));
     float y = bitsf(0x7EF311C3u - fbits(a));
-    y = fmul(y, fsub(2.0f, fmul(a, y)));
-    y = fmul(y, fsub(2.0f, fmul(a, y)));
-    y = fadd(fmul(y, fsub(1.0f, fmul(a, y))), y);
+    y = y * (2.0f - a * y);
+    y = y * (2.0f - a * y);
+    y = y * (1.0f - a * y) + y;
     int32_t k = 127 - (int32_t)(mag >> 23);
     return bitsf((uint32_t)((int32_t)fbits(y) + k * (1 << 23)) | sign);
 }
 
-// q8: round half to even, saturate to +-127, NaN -> 0
+// q8: round half to even, saturate to +-127, NaN -> 0.  v_rndne_f32, then v_cvt_i32_f32 (which
+// converts NaN to 0 and saturates out-of-range values and infinities), then a clamp; a
+// denormal rounds to zero with or without its flush.
 __device__ __forceinline__ int q8(float x) {
-    x = ftz(x);
-    if (x != x) return 0;
-    float r = __builtin_rintf(x);
-    r = r > 127.0f ? 127.0f : (r < -127.0f ? -127.0f : r);
-    return (int)r;
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(__builtin_rintf(x)));
+    return min(max(r, -127), 127);
 }
 
 __device__ __forceinline__ int window_of(int fmt) {
