@@ -21,6 +21,37 @@ constexpr int FOLD_C = 256;                       // elements a range
 constexpr int FOLD_PPR = FOLD_C / 32;             // 16-byte pieces a range
 constexpr int FOLD_NRMAX = QIN_KMAX / FOLD_C;     // ranges a row
 
+// lane 8 g's x of each team of T lanes (g < T / 8), at the team's first lane: DPP row_ror:8
+// moves lane 8 to lane 0 within a row of 16; v_permlane16_swap of (x, x) returns the other row
+// of each row pair in its second half, v_permlane32_swap the other half-wave
+__device__ __forceinline__ float ror8(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_swap16(float x) {
+    return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+}
+__device__ __forceinline__ float half_swap32(float x) {
+    return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+}
+template <int T>
+__device__ __forceinline__ void gather8(float x, float (&v)[T / 8]) {
+    v[0] = x;
+    v[1] = ror8(x);
+    if constexpr (T >= 32) {
+        const float h = row_swap16(x);
+        v[2] = h;
+        v[3] = ror8(h);
+    }
+    if constexpr (T == 64) {
+        const float q = half_swap32(x);
+        v[4] = q;
+        v[5] = ror8(q);
+        const float qh = row_swap16(q);
+        v[6] = qh;
+        v[7] = ror8(qh);
+    }
+}
+
 template <int FMT, int L, int T>
 __device__ __forceinline__ void fold_body(const MMArgs& a) {
     static_assert(FMT != OTPU_INT8, "4-bit weights");
@@ -171,15 +202,19 @@ __device__ __forceinline__ void fold_body(const MMArgs& a) {
             // the finished Sa * 2^-W need no operand flush
             yr[i] = fmul_f(fmul_f((float)s, st.sw), sa2[i]);
         }
+        // the team's first lane gathers the ranges' outputs (lanes team T + 8 g of slot i hold
+        // range i GPT + g) and adds them in range order; the outputs are fmul results, flushed
         float y = 0.0f;
 #pragma unroll
-        for (int i = 0; i < L; ++i)
+        for (int i = 0; i < L; ++i) {
+            float v[GPT];
+            gather8<T>(yr[i], v);
 #pragma unroll
             for (int g = 0; g < GPT; ++g) {
                 const int r = i * GPT + g;
-                const float v = __shfl(yr[i], team * T + g * FOLD_PPR, 64);
-                if (r < NR) y = r ? fadd(y, v) : v;
+                if (r < NR) y = r ? fadd_f(y, v[g]) : v[g];
             }
+        }
         if (tl == 0 && n < a.N) a.out[n] = y;
     }
 }

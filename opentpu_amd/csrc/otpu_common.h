@@ -34,6 +34,8 @@ __device__ __forceinline__ float fmul(float a, float b) { return fin(ftz(a) * ft
 // fmul for operands already flushed (a fin() result, a flushed load, an integer's float)
 __device__ __forceinline__ float fmul_f(float a, float b) { return fin(a * b); }
 __device__ __forceinline__ float fadd(float a, float b) { return fin(ftz(a) + ftz(b)); }
+// fadd for operands already flushed
+__device__ __forceinline__ float fadd_f(float a, float b) { return fin(a + b); }
 __device__ __forceinline__ float fsub(float a, float b) { return fin(ftz(a) - ftz(b)); }
 __device__ __forceinline__ float pow2f(int d) { return bitsf((uint32_t)(d + 127) << 23); }
 
