@@ -336,8 +336,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=80)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c3r,c4,c5,copy (default: c1,c2s,c3,c4,c5; "
-                    "c3r: the ROW GEMM alone); "
+    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c3r,c3m,c4,c5,copy (default: c1,c2s,c3,c4,c5; "
+                    "c3r / c3m: the ROW / the MX GEMM alone); "
                     "the headline c2 always runs, c2s adds its single-launch figure")
     ap.add_argument("--summarize", metavar="DIR", help="print a text summary of rocprofv3 CSV output and exit")
     args = ap.parse_args()
@@ -405,7 +405,7 @@ def main():
         msf = timed(lambda: o3.fill_(1.0), 20, 2, torch.cuda.current_stream())
         del o3
         extra["c3_output_write_alone"] = {"us": round(msf * 1e3, 2), "what": "torch fill_ of the 512 x 8192 fp32 output"}
-    if "c3" in only:
+    if "c3" in only or "c3m" in only:
         ms3m = gemm(5, 1, row_mode=False)
         tops = 2 * 512 * 2048 * 8192 / (ms3m * 1e-3) / 1e12
         extra["c3_gemm_mx_x_rsc"] = {"us": round(ms3m * 1e3, 2), "TOPS": round(tops, 2),

@@ -43,8 +43,9 @@ constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds
 
 // rows a team takes per iteration: 8 rows' loads in flight per wave for one activation row
 // with one piece a lane (measured on MI355X: 16 the same for the 80-problem launches, 8 faster
-// for small grids), 4 when that still leaves CUs idle (R_SMALL); 8 a team with four or more
-// pieces a lane (the LM head: 4% over 2); fewer as activation rows add sums to carry
+// for small grids), 4 when that still leaves CUs idle (R_SMALL); 4 a team with four or more
+// pieces a lane (the LM head: 105.4 against 106.0 us at 8 over three paired runs, 4% over 2);
+// fewer as activation rows add sums to carry
 #ifndef OTPU_GEMV_R1
 #define OTPU_GEMV_R1 8
 #endif
@@ -55,7 +56,7 @@ constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds
 #define OTPU_GEMV_R2 2
 #endif
 #ifndef OTPU_GEMV_R4
-#define OTPU_GEMV_R4 8
+#define OTPU_GEMV_R4 4
 #endif
 constexpr int rows_per_team_rt(int L, int mr) {
     return L >= 4 ? (OTPU_GEMV_R4 / mr > 0 ? OTPU_GEMV_R4 / mr : 1) : (L == 1 ? OTPU_GEMV_R1 / mr : OTPU_GEMV_R2);

@@ -315,6 +315,28 @@ def test_gemv_row_blocking_paths(ops, fmt, rsc, K):
         assert same_bits(one, want[b])
 
 
+@pytest.mark.parametrize("fmt,K,rsc", [("int8", 4096, False), ("int8", 2560, True), ("int4", 8192, False),
+                                       ("fp4", 8192, False)])
+def test_gemv_four_or_more_pieces_a_lane(ops, fmt, K, rsc):
+    """Rows of 4 or more 16-byte pieces a lane (the LM head's shape class), 1 to 4 activation
+    rows a launch (the register tiling's MR 1, 2 and 4), against the C oracle."""
+    _, _, mxu = ops
+    rng = np.random.default_rng(K + len(fmt) + rsc)
+    N = 300
+    W = (spread(rng, N, K, 1.5, 128) * 0.02).astype(np.float32)
+    if fmt == "int8":
+        rows, srows = Q.pack_rsc(W) if rsc else Q.pack_int8x(W)
+    else:
+        rows, srows = Q.quantize_mxu(W, fmt)
+    for M in (1, 2, 3, 4):
+        x = spread(rng, M, K, 2.0, 32)
+        q, Sa, da = F.quantize_mx(x, 32)
+        say("gemv many pieces", fmt, K, rsc, M)
+        got = mxu.mm(q, Sa, da, rows, srows, fmt, K, rsc=rsc)
+        want = OC.mm(q, Sa, da, rows, srows, fmt, K, flags=MM.RSC if rsc else 0)
+        assert same_bits(got, want)
+
+
 def test_headline_batched_c2_full_size(ops):
     """The bench's timed headline launch itself: 80 independent c2 GEMVs (int4x N=6144 K=2048,
     weights N(0, 0.02) packed on the GPU, MX activations of N(0, 1) rows) in one otpu_mm_batched
