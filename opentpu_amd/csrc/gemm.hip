@@ -420,110 +420,93 @@ __device__ __forceinline__ void gemm_pass_mp(const GemmArgs& a, int8_t* ring, co
     ring_barrier();
 }
 
-// A full tile leaves through LDS: each wave writes its 64 x 64 values in the MFMA layout (rows
-// 68 floats apart: the 4 row groups of a write land on distinct banks) and reads them back as
-// float4 rows, so every store instruction writes 4 rows x 256 contiguous bytes.  `lds` is the
-// ring's memory (every wave is past its last read of the ring when the epilogue starts).
-constexpr int TPS = 68;                         // transpose row stride, floats
+// The epilogue of a tile whose MM integers are acc << sh (acc the int32 sums, sh = 16 - smax >= 0):
+// y = (i2f(acc << sh) * Sw[n]) * (Sa[m] * 2^-16), then ACC / ASCALE.  i2f(acc << sh) is the int32's
+// RNE float times 2^sh exactly.  sa2: the tile's rows' Sa * 2^-16 in LDS (row r of the tile at r).
+// A full tile leaves through LDS: each wave writes its 64 x 64 accumulators in the MFMA layout
+// (rows 68 words apart: the 4 row groups of a write land on distinct banks) and reads them back
+// as 4-column rows, so every store instruction writes 4 rows x 256 contiguous bytes.  The scaling
+// runs after the transpose, in a loop over the 16 row groups a lane stores: the tile runs once per
+// CU from a cold instruction cache, so the epilogue's code length is its latency (unrolled over
+// all 64 values it was 128 rounded products of straight-line code).  `lds` is the ring's memory
+// (every wave is past its last read of the ring when the epilogue starts).
+constexpr int TPS = 68;                         // transpose row stride, words
 
-__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int8_t* lds, int m0, int n0, float (&v)[4][4][4],
-                                              const float (&sw)[4], const float (&sa2)[4][4]) {
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int8_t* lds, const float* sa2, int m0, int n0,
+                                              const v4i (&acc)[4][4], int sh) {
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int mb = m0 + (wid >> 1) * 64 + 4 * (lane >> 4), nb = n0 + (wid & 1) * 64 + (lane & 15);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int t = 0; t < 4; ++t) v[i][j][t] = fmul(fmul(v[i][j][t], sw[j]), sa2[i][t]);
+    const bool unit = (a.flags & OTPU_UNIT) != 0;
     const bool full = m0 + GBM <= a.M && n0 + GBN <= a.N;
     if (full && a.vec4) {
-        float* T = reinterpret_cast<float*>(lds) + wid * 64 * TPS;
+        int* T = reinterpret_cast<int*>(lds) + wid * 64 * TPS;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int t = 0; t < 4; ++t) T[(16 * i + 4 * (lane >> 4) + t) * TPS + 16 * j + (lane & 15)] = v[i][j][t];
+                for (int t = 0; t < 4; ++t) T[(16 * i + 4 * (lane >> 4) + t) * TPS + 16 * j + (lane & 15)] = acc[i][j][t];
         const int q = lane & 15, g = lane >> 4;
-        const int mr = m0 + (wid >> 1) * 64 + g, nc = n0 + (wid & 1) * 64 + 4 * q;
-        float4 y[16];
+        const int rt = (wid >> 1) * 64 + g;                      // the tile row of group s = 0
+        const int nc = n0 + (wid & 1) * 64 + 4 * q;
+        float sw[4];
 #pragma unroll
-        for (int s = 0; s < 16; ++s) y[s] = *reinterpret_cast<const float4*>(T + (g + 4 * s) * TPS + 4 * q);
-        if (a.flags & (OTPU_ACC | OTPU_ASCALE)) {
-            float4 old[16];
-#pragma unroll
-            for (int s = 0; s < 16; ++s) old[s] = *reinterpret_cast<const float4*>(a.out + (int64_t)(mr + 4 * s) * a.ors + nc);
-            const bool asc = (a.flags & OTPU_ASCALE) != 0;
-#pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const float al = asc ? a.alpha[mr + 4 * s] : 1.0f;
-                if (asc) {
-                    y[s].x = fadd(fmul(old[s].x, al), y[s].x); y[s].y = fadd(fmul(old[s].y, al), y[s].y);
-                    y[s].z = fadd(fmul(old[s].z, al), y[s].z); y[s].w = fadd(fmul(old[s].w, al), y[s].w);
-                } else {
-                    y[s].x = fadd(old[s].x, y[s].x); y[s].y = fadd(old[s].y, y[s].y);
-                    y[s].z = fadd(old[s].z, y[s].z); y[s].w = fadd(old[s].w, y[s].w);
-                }
-            }
-        }
-#pragma unroll
+        for (int c = 0; c < 4; ++c) sw[c] = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(a.ws + (int64_t)(nc + c) * a.srs));
+        const bool asc = (a.flags & OTPU_ASCALE) != 0, accf = (a.flags & OTPU_ACC) != 0;
+#pragma unroll 2
         for (int s = 0; s < 16; ++s) {
-            float* p = a.out + (int64_t)(mr + 4 * s) * a.ors + nc;
+            const int r = rt + 4 * s;
+            const int4 raw = *reinterpret_cast<const int4*>(T + (g + 4 * s) * TPS + 4 * q);
+            const float sa = sa2[r];
+            float y[4] = {ldexpf((float)raw.x, sh), ldexpf((float)raw.y, sh), ldexpf((float)raw.z, sh),
+                          ldexpf((float)raw.w, sh)};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) y[c] = fmul_f(fmul_f(y[c], sw[c]), sa);
+            float* p = a.out + (int64_t)(m0 + r) * a.ors + nc;
+            if (asc || accf) {
+                const float4 old = *reinterpret_cast<const float4*>(p);
+                const float o[4] = {old.x, old.y, old.z, old.w};
+                const float al = asc ? a.alpha[m0 + r] : 1.0f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) y[c] = asc ? fadd(fmul(o[c], al), y[c]) : fadd(o[c], y[c]);
+            }
 #ifndef OTPU_GEMM_NT_STORE
 #define OTPU_GEMM_NT_STORE 1
 #endif
 #if OTPU_GEMM_NT_STORE
             typedef float f32x4 __attribute__((ext_vector_type(4)));
-            __builtin_nontemporal_store(f32x4{y[s].x, y[s].y, y[s].z, y[s].w}, reinterpret_cast<f32x4*>(p));
+            __builtin_nontemporal_store(f32x4{y[0], y[1], y[2], y[3]}, reinterpret_cast<f32x4*>(p));
 #else
-            *reinterpret_cast<float4*>(p) = y[s];
+            *reinterpret_cast<float4*>(p) = make_float4(y[0], y[1], y[2], y[3]);
 #endif
         }
         return;
     }
-    if (a.flags & (OTPU_ACC | OTPU_ASCALE)) {
-        float old[4][4][4];
+    // a partial tile (or an unaligned output): each lane's own values, in the MFMA layout
+    const int mb = m0 + (wid >> 1) * 64 + 4 * (lane >> 4), nb = n0 + (wid & 1) * 64 + (lane & 15);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int m = mb + i * 16 + t, n = nb + j * 16;
-                    old[i][j][t] = (m < a.M && n < a.N) ? a.out[(int64_t)m * a.ors + n] : 0.0f;
-                }
-        const bool asc = (a.flags & OTPU_ASCALE) != 0;
+    for (int j = 0; j < 4; ++j) {
+        const int n = nb + j * 16;
+        const float sw = (unit || n >= a.N) ? 1.0f : ftz(*reinterpret_cast<const float*>(a.ws + (int64_t)n * a.srs));
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int m = mb + i * 16 + t;
-                const float al = (asc && m < a.M) ? a.alpha[m] : 1.0f;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    v[i][j][t] = asc ? fadd(fmul(old[i][j][t], al), v[i][j][t]) : fadd(old[i][j][t], v[i][j][t]);
+                if (m >= a.M || n >= a.N) continue;
+                float y = fmul_f(fmul_f(ldexpf((float)acc[i][j][t], sh), sw), sa2[m - m0]);
+                float* o = a.out + (int64_t)m * a.ors + n;
+                if (a.flags & OTPU_ASCALE) y = fadd(fmul(*o, a.alpha[m]), y);
+                else if (a.flags & OTPU_ACC) y = fadd(*o, y);
+                *o = y;
             }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int m = mb + i * 16 + t;
-            float* row = a.out + (int64_t)m * a.ors;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int n = nb + j * 16;
-                if (full || (m < a.M && n < a.N)) row[n] = v[i][j][t];
-            }
-        }
 }
 
 // a tile of plain weights whose activation groups hold NP offsets d (planes s = d): one K walk
 // (gemm_pass_mp), the planes' sums combined, then the epilogue
 template <int NP>
 __device__ __forceinline__ void gemm_tile_mp(const GemmArgs& a, int8_t* ring, const uint32_t* da_lds, int m0, int n0,
-                                             uint32_t dmask, int smax, const float (&sw)[4], const float (&sa2)[4][4]) {
+                                             uint32_t dmask, int smax, const float* sa2) {
     int dv[MP_MAX];
     uint32_t left = dmask;
 #pragma unroll
@@ -540,7 +523,6 @@ __device__ __forceinline__ void gemm_tile_mp(const GemmArgs& a, int8_t* ring, co
             for (int j = 0; j < 4; ++j) acc[p][i][j] = v4i{0, 0, 0, 0};
     gemm_pass_mp<NP>(a, ring, da_lds, acc, dv, m0, n0);
     // sum_p C_p << (smax - d_p) = C << (16 - smax) with C an int32 (the bound checked by the caller)
-    float v[4][4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -548,17 +530,15 @@ __device__ __forceinline__ void gemm_tile_mp(const GemmArgs& a, int8_t* ring, co
             v4i t = acc[0][i][j] << (smax - dv[0]);
 #pragma unroll
             for (int p = 1; p < NP; ++p) t += acc[p][i][j] << (smax - dv[p]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[i][j][e] = ldexpf((float)t[e], 16 - smax);
+            acc[0][i][j] = t;
         }
-    tile_epilogue(a, ring, m0, n0, v, sw, sa2);
+    tile_epilogue(a, ring, sa2, m0, n0, acc[0], 16 - smax);
 }
 
 // a tile's planes in ascending s (Horner in the int32 accumulators), then its epilogue
 template <bool MA, bool MB>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int m0, int n0, uint32_t dmask,
-                                          uint32_t emask, uint32_t smask, int smin, int smax, const float (&sw)[4],
-                                          const float (&sa2)[4][4]) {
+                                          uint32_t emask, uint32_t smask, int smin, int smax, const float* sa2) {
     v4i acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -583,14 +563,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int
         }
     }
     // acc = C << (16 - smax) with C an int32: i2f(acc) = rne(C) * 2^(16 - smax), exactly
-    float v[4][4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int t = 0; t < 4; ++t) v[i][j][t] = ldexpf((float)acc[i][j][t], 16 - smax);
-    tile_epilogue(a, sm.ring, m0, n0, v, sw, sa2);
+    tile_epilogue(a, sm.ring, sa2, m0, n0, acc, 16 - smax);
 }
 
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
@@ -599,9 +572,9 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     __shared__ uint8_t sDw[2][GBN];        // the stage's dw byte per weight row
     __shared__ uint32_t sMask[8];          // per wave: d values and e values present in the tile
     __shared__ uint32_t sDaAll[GBM * DAS]; // the tile's offset words (K <= 4096), for gemm_pass_mp
+    __shared__ float sSa2[GBM];            // the tile rows' Sa * 2^-16
 
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wid >> 1, wn = wid & 1;
 
     // XCD-major tile order: workgroup b runs on XCD b % 8; give each XCD whole weight panels
     int b = blockIdx.x, tm, tn;
@@ -624,22 +597,10 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     // epilogue constants (a masked tile waits for them before reusing the ring)
     ring_prologue(a, sRing, m0, n0);
 
+    // the tile rows' Sa * 2^-16 for the epilogue (written before the scan's barrier)
+    if (tid < GBM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-16)) : 0.0f;
     // the offsets present in this tile: d over its activation rows, e over its weight rows.
     // Two threads a row; the loads of a thread are independent (issued back to back).
-    // epilogue constants of this lane's outputs (loaded now, used after the K loop)
-    float sw[4], sa2[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn * 64 + j * 16 + (lane & 15);
-        sw[j] = (unit || n >= a.N) ? 1.0f : *reinterpret_cast<const float*>(a.ws + (int64_t)n * a.srs);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int m = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + t;
-            sa2[i][t] = m < a.M ? a.Sa[m] : 0.0f;
-        }
     {
         uint32_t dm = 0, em = 0;
         const int r = tid & (GBM - 1), h = tid >> 7;
@@ -690,22 +651,15 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     for (int d = 0; d <= 16; ++d)
         if (dmask >> d & 1) smask |= (emask << d) & 0x1FFFFu;
 
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) sa2[i][t] = fmul(sa2[i][t], pow2f(-16));
-
     if (smask == 0) {                               // every group drops: acc = 0
         wait_dma<0>();                              // (the ring prologue's loads end in LDS)
         ring_barrier();
-        float v[4][4][4];
+        v4i z[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) v[i][j][t] = 0.0f;
-        tile_epilogue(a, sRing, m0, n0, v, sw, sa2);
+            for (int j = 0; j < 4; ++j) z[i][j] = v4i{0, 0, 0, 0};
+        tile_epilogue(a, sRing, sSa2, m0, n0, z, 0);
         return;
     }
     const int smin = __builtin_ctz(smask), smax = 31 - __builtin_clz(smask);
@@ -732,23 +686,23 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     const Smem sm{reinterpret_cast<int8_t(*)[GBM * GBK]>(sRing),
                   reinterpret_cast<int8_t(*)[GBN * GBK]>(sRing + 2 * GBM * GBK), sDa, sDw, sRing};
     if (single) {
-        gemm_tile<false, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
+        gemm_tile<false, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sSa2);
         return;
     }
     // plain weights, up to MP_MAX activation planes: one K walk through the ring for all of them
     const int np = __builtin_popcount(dmask);
     if (plain && KT <= MP_KT && np >= 1 && np <= MP_MAX) {
         switch (np) {
-            case 1: gemm_tile_mp<1>(a, sRing, sDaAll, m0, n0, dmask, smax, sw, sa2); break;
-            case 2: gemm_tile_mp<2>(a, sRing, sDaAll, m0, n0, dmask, smax, sw, sa2); break;
-            default: gemm_tile_mp<3>(a, sRing, sDaAll, m0, n0, dmask, smax, sw, sa2); break;
+            case 1: gemm_tile_mp<1>(a, sRing, sDaAll, m0, n0, dmask, smax, sSa2); break;
+            case 2: gemm_tile_mp<2>(a, sRing, sDaAll, m0, n0, dmask, smax, sSa2); break;
+            default: gemm_tile_mp<3>(a, sRing, sDaAll, m0, n0, dmask, smax, sSa2); break;
         }
         return;
     }
     wait_dma<0>();                                  // the masked passes reuse the ring's memory
     ring_barrier();
-    if (plain) gemm_tile<true, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
-    else gemm_tile<true, true>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sw, sa2);
+    if (plain) gemm_tile<true, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sSa2);
+    else gemm_tile<true, true>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sSa2);
 }
 
 }  // namespace otpu
