@@ -190,15 +190,18 @@ def gemm(steps, warmup, row_mode=True):
     return timed(step, steps, warmup, torch.cuda.current_stream())
 
 
-def c4_step(steps, warmup):
+def c4_step(steps, warmup, persistent=True):
     """The chained decode step (28 Qwen3-0.6B-shaped layers of int4x linears, weights seeded
     100 + layer): two resident copies of the weights (474 MB, more than the Infinity Cache),
-    steps alternating between them, every step's kernels replayed from one HIP graph."""
+    steps alternating between them, every step's kernels replayed from one HIP graph.
+    persistent: the step as one otpu_chain_step launch (the default path), else 112 launches."""
     import torch
 
     from opentpu_amd.chain import DecodeChain, Shape
     sh = Shape()
     chains = [DecodeChain.synthetic(sh, "int4", seed0=100) for _ in range(2)]
+    for c in chains:
+        c.persistent = persistent
     x = torch.randn((1, sh.hidden), generator=torch.Generator(device="cuda").manual_seed(4), device="cuda")
     for c in chains:
         c.x.copy_(x)
@@ -394,6 +397,9 @@ def main():
     if "c4" in only:
         extra["c4_decode_step"] = c4_step(10, 2)
         print(f"[c4] {extra['c4_decode_step']}", file=sys.stderr, flush=True)
+        # the same step as one launch per linear (the path the persistent step replaces)
+        extra["c4_decode_step_launches"] = c4_step(10, 2, persistent=False)
+        print(f"[c4 launches] {extra['c4_decode_step_launches']}", file=sys.stderr, flush=True)
     if "c3" in only or "c3r" in only:
         ms3 = gemm(5, 1)
         tops = 2 * 512 * 2048 * 8192 / (ms3 * 1e-3) / 1e12

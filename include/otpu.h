@@ -178,6 +178,32 @@ int otpu_mm_spl(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da
 int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float* old, float* out,
                   otpu_stream_t stream);
 
+/* The fused, folded decode chain in one persistent launch (per layer: MM qkv, MM o on q, MM
+ * gate/up, the folded down projection on mul(g, u), each with its input row's QACT in the
+ * prologue: opentpu/kernels/mlp.py's layer and Builder.dot's per-range MMs + ACC,
+ * opentpu/compiler.py:2686-2720), bit for bit the outputs of otpu_mm_qin x 3 + otpu_mm_qin_fold a
+ * layer.  The reference runs this as an ISA program; this is the same computation as one launch
+ * of one workgroup a CU, the phases handing rows to each other through the plan's memory.
+ *   otpu_chain_plan_bytes: the plan's size (-1 for bad dimensions).
+ *   otpu_chain_plan: checks every phase as its one-launch entry point would and writes the plan
+ *   (synchronous; plan device memory, 256-byte aligned).  w / rs / ws / srs / outs: 4 a layer in
+ *   the order qkv, o, gu, down (each layer's strides equal layer 0's); rnorm: RSCALE factors
+ *   [layers, 2] (device) or NULL; cscale: 2 a layer (gamma of the qkv and the gate/up QACTs,
+ *   device, entries may be NULL) or NULL; x: the step's input row [hidden]; outs: the phases' fp32
+ *   output rows (qkv [q_dim + 2 kv_dim], o [hidden], gu [2 F], down [hidden]).  int4x or fp4x6
+ *   weights; hidden <= 1024, q_dim <= 2048, F a multiple of 256 and <= 3072, hidden and q_dim
+ *   multiples of 32.
+ *   otpu_chain_step: one step (reads x, writes every output row); capturable in a HIP graph.
+ *   otpu_chain_error: the plan's error word (0: every hand-off completed; 1: a wait ran out of
+ *   polls, the outputs since are invalid), synchronous. */
+int64_t otpu_chain_plan_bytes(int layers, int hidden, int q_dim, int kv_dim, int F);
+int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int fmt, const uint8_t* const* w,
+                    const int64_t* rs, const uint8_t* const* ws, const int64_t* srs, const float* rnorm,
+                    const float* const* cscale, const float* x, float* const* outs, void* plan,
+                    int64_t plan_bytes);
+int otpu_chain_step(const void* plan, otpu_stream_t stream);
+int otpu_chain_error(const void* plan, uint32_t* err);
+
 /* B independent MMs of one shape in one launch (a layer stack's or an expert set's decode
  * GEMVs): problem b's operands start at the given pointers plus b times the *_bstride
  * (elements of each pointer's type; bytes for w and ws).  No ACC / ASCALE / RMAX. */

@@ -61,7 +61,10 @@ class Shape:
 class DecodeChain:
     """`layers`: per layer a dict name -> (rows, srows) device tensors (uint8).
 
-    fused (default): a layer is four kernels, each linear an otpu_mm_qin (the QACT of its input
+    persistent (default where it applies: fused and folded, int4 / fp4 weights, hidden <= 1024,
+    q_dim <= 2048, F <= 3072): the whole step is one launch of otpu_chain_step, its phases handing
+    rows to each other on the GPU; the same bits as the four kernels a layer below.
+    fused: a layer is four kernels, each linear an otpu_mm_qin (the QACT of its input
     row in the GEMV's prologue).  With 4-bit weights and 256-column down chunks the down
     projection is one otpu_mm_qin_fold, which folds its chunks' outputs in chunk order (the ACC
     chain) itself; otherwise its per-chunk outputs stay partial, the next layer's prologue folds
@@ -72,7 +75,7 @@ class DecodeChain:
     FUSED_KERNELS_PER_LAYER = 4    # fused: one QACT + MM kernel per linear
 
     def __init__(self, layers: list, shape: Shape = Shape(), fmt: str = "int4", fused: bool = True,
-                 norms: list | None = None):
+                 norms: list | None = None, persistent: bool | None = None):
         """norms (optional): per layer (gamma_attn, gamma_mlp), the RMSNorm weights [hidden] in
         front of the qkv and of the gate / up projections.  They ride in those linears' QACT as
         CSCALE, with the row factor r of each norm (RSCALE: `self.rnorm[l, 0 | 1]`, 1 unless
@@ -111,6 +114,11 @@ class DecodeChain:
             self.norms = [tuple(X.dev(g, np.float32).reshape(-1) for g in pair) for pair in norms]
         self.rnorm = T.ones((len(layers), 2), dtype=f32, device=dev)
         self._graph = None
+        self._plan = None
+        self.persistent = self.persistent_fits() if persistent is None else bool(persistent)
+        if self.persistent and not self.persistent_fits():
+            raise ValueError("DecodeChain: the persistent step needs fused, folded int4 / fp4 layers with "
+                             "hidden <= 1024, q_dim <= 2048, F <= 3072")
 
     @staticmethod
     def synthetic(shape: Shape = Shape(), fmt: str = "int4", seed0: int = 100, std: float = 0.02,
@@ -206,15 +214,71 @@ class DecodeChain:
                rows.shape[1], X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(y),
                X.stream())
 
+    # --- the persistent step ---------------------------------------------------------------
+    def persistent_fits(self) -> bool:
+        """Whether otpu_chain_step can run this chain (its phases' teams are compiled in)."""
+        s = self.shape
+        return (self.fused and self.fold and self.fmt in ("int4", "fp4") and s.hidden <= 1024 and s.hidden % 32 == 0
+                and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 3072 and s.F % 256 == 0)
+
+    def _use_persistent(self) -> bool:
+        return self.persistent and self.fused and self.fold
+
+    def _plan_ptr(self) -> int:
+        """The plan of otpu_chain_step (built once: the weights and every row buffer are fixed)."""
+        if self._plan is not None:
+            return self._plan[1]
+        import ctypes as C
+        s, n = self.shape, len(self.layers)
+        lib = X.load()
+        nbytes = lib.otpu_chain_plan_bytes(n, s.hidden, s.q_dim, s.kv_dim, s.F)
+        if nbytes <= 0:
+            raise ValueError("DecodeChain: no persistent plan for this shape")
+        T = X.torch()
+        buf = T.empty((nbytes + 256,), dtype=T.uint8, device="cuda")
+        ptr = (buf.data_ptr() + 255) // 256 * 256
+        P = C.c_void_p * (4 * n)
+        I64 = C.c_int64 * (4 * n)
+        w, ws, outs = P(), P(), P()
+        rs, srs = I64(), I64()
+        cs = (C.c_void_p * (2 * n))() if self.norms is not None else None
+        for l in range(n):
+            dst = self.y if l == n - 1 else self.hbuf[l % 2]
+            for k, (name, out) in enumerate((("qkv", self.qkv), ("o", self.o), ("gu", self.gu), ("down", dst))):
+                rows, srows = self.layers[l][name]
+                j = 4 * l + k
+                w[j], ws[j], outs[j] = X.ptr(rows), X.ptr(srows), X.ptr(out)
+                rs[j], srs[j] = rows.shape[1], srows.shape[1]
+            if cs is not None:
+                cs[2 * l], cs[2 * l + 1] = X.ptr(self.norms[l][0]), X.ptr(self.norms[l][1])
+        X.call("otpu_chain_plan", n, s.hidden, s.q_dim, s.kv_dim, s.F, X.FMT[self.fmt], w, rs, ws, srs,
+               X.ptr(self.rnorm) if self.norms is not None else None, cs, X.ptr(self.x), outs, ptr, nbytes)
+        self._plan = (buf, ptr)
+        return ptr
+
+    def chain_error(self) -> int:
+        """The persistent plan's error word (0: every hand-off of every step so far completed)."""
+        if self._plan is None:
+            return 0
+        import ctypes as C
+        e = C.c_uint32(0)
+        X.call("otpu_chain_error", self._plan[1], C.byref(e))
+        return int(e.value)
+
     @property
     def kernels_per_step(self) -> int:
         n = len(self.layers)
+        if self.fused and self._use_persistent():
+            return 1
         if not self.fused:
             return n * self.KERNELS_PER_LAYER
         return n * self.FUSED_KERNELS_PER_LAYER + (0 if self.fold else 1)  # + the last otpu_acc_rows
 
     def _queue(self) -> None:
         n = len(self.layers)
+        if self._use_persistent():
+            X.call("otpu_chain_step", self._plan_ptr(), X.stream())
+            return
         if self.fused and self.fold:
             src = self.x
             for l in range(n):

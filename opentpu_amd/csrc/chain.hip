@@ -1,0 +1,247 @@
+// The chained decode step of a stack of 4-bit quantized linears in one persistent launch: per
+// layer MM qkv, MM o (on q), MM gate/up and the folded down projection on mul(g, u), each with
+// the QACT of its input row in the prologue (the fused chain's four kernels a layer,
+// `opentpu/kernels/mlp.py`, `Builder.dot` `opentpu/compiler.py:2686-2720`), bit for bit what
+// otpu_mm_qin / otpu_mm_qin_fold compute one launch at a time.
+//
+// Why one launch.  In a chain of 112 dependent launches each costs ~5 us for 1-3 MB of weights:
+// the dispatch gap, the input row's first read, and the code fetched cold each time.  Here one
+// workgroup a CU runs every phase of the step; a phase hands its output row to the next as
+// 8-byte entries (tag << 32 | fp32 bits) written with device-scope stores and read with
+// device-scope loads (they bypass the XCDs' non-coherent L2s) until every entry carries the
+// phase's tag: no fences, no counters, no grid barrier (one with agent-scope release / acquire
+// costs ~30 us on MI355X, a hand-off ~2-3 us).  A phase issues its first weight rows before it
+// waits, so the weights stream in during the hand-off.  Two entry rows alternate: a workgroup
+// writes phase i + 2 into the row phase i used only after reading all of phase i + 1 (o waits
+// for k and v as well), which its producers wrote after they had read phase i; a workgroup
+// without rows in a phase reads nothing in it.
+//
+// Tags.  Phase i of a call carries tag E * 4 L + i + 1, E the call's number: every workgroup
+// keeps its own call counter (read at the start, advanced at the end), so graph replays of the
+// same launch get fresh tags with no host involvement.  Every wait is bounded: one that runs out
+// of polls sets the plan's error word and the step goes on (its output is then invalid).
+//
+// Phases' teams (compile-time): qkv and gate/up 32 lanes a row (K <= 1024), o 64 lanes
+// (K <= 2048), the down projection 32 lanes with 3 pieces each (F <= 3072, F-chunks of 256).
+#include <algorithm>
+#include <vector>
+
+#include "gemv_fold.h"
+
+namespace otpu {
+
+int qin_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float* rscale, const float* cscale,
+             int nsum, int64_t sum_stride, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
+             int64_t srs, int N, int fmt, int flags, int k0, float* out, int64_t ors, int64_t part_stride);
+int fold_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float* rscale, const float* cscale,
+              int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
+              float* out);
+
+constexpr int CHAIN_SLOTS = 4096;               // workgroups' call counters a plan holds
+constexpr int CHAIN_SPIN = 1 << 16;             // polls a wait allows (~1 us each)
+constexpr int CHAIN_PAD_LDS = 96 * 1024;        // dynamic LDS that keeps one workgroup a CU
+
+// the phases' teams: T lanes a row, R rows a team (the prologue QACT holds K <= 32 T elements)
+#ifndef OTPU_CHAIN_R
+#define OTPU_CHAIN_R 4
+#endif
+constexpr int QKV_T = 32, QKV_R = OTPU_CHAIN_R; // (the gate/up phase's body too: one copy of the code)
+#ifndef OTPU_CHAIN_OR
+#define OTPU_CHAIN_OR 1
+#endif
+constexpr int O_T = 64, O_R = OTPU_CHAIN_OR;
+constexpr int GU_T = QKV_T, GU_R = QKV_R;
+constexpr int DN_T = 32, DN_L = 3;
+
+struct ChainLayer {                              // the pointers of one layer (qkv, o, gu, down)
+    const uint8_t* w[4];
+    const uint8_t* ws[4];
+    const float* cs[2];                          // CSCALE of the qkv and the gate/up QACTs (or NULL)
+    float* out[4];                               // the phases' plain output rows
+};
+
+struct ChainPlan {                               // device memory: the header, then the layers
+    MMArgs kind[4];                              // per phase: shape, strides and team (pointers per layer)
+    const float* x0;                             // the step's input row
+    const float* rnorm;                          // RSCALE factors [layers, 2] or NULL
+    const ChainLayer* layer;
+    uint64_t* ll[2];                             // the alternating entry rows
+    uint32_t* calls;                             // call counter per workgroup
+    uint32_t* err;
+    int layers, fmt;
+};
+
+// rows of phase kind k the first iteration of workgroup b covers start at b * rows_per_wg(k)
+__device__ __forceinline__ int rows_per_wg(int k) {
+    return k == 0 ? 4 * (64 / QKV_T) * QKV_R : k == 1 ? 4 * (64 / O_T) * O_R : k == 2 ? 4 * (64 / GU_T) * GU_R : 4 * (64 / DN_T);
+}
+
+union ChainLds {
+    QinLds q;
+    FoldLds f;
+};
+
+template <int FMT>
+__device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
+    const int b = blockIdx.x;
+    const uint32_t E = __hip_atomic_load(P.calls + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int NL = P.layers;
+    const uint32_t t0 = E * (uint32_t)(4 * NL);
+    for (int l = 0; l < NL; ++l) {
+        const ChainLayer& ly = P.layer[l];
+#pragma unroll 1
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * l + k;
+            MMArgs a = P.kind[k];
+            if (b * rows_per_wg(k) >= a.N) continue;     // no rows here: nothing to wait for
+            a.w = ly.w[k];
+            a.ws = ly.ws[k];
+            a.out = ly.out[k];
+            a.ll_in = i ? P.ll[(i - 1) & 1] : nullptr;
+            a.xin = P.x0;
+            a.ll_out = P.ll[i & 1];
+            a.tag_in = t0 + (uint32_t)i;
+            a.tag_out = t0 + (uint32_t)i + 1;
+            a.err = P.err;
+            a.spin = CHAIN_SPIN;
+            a.ll_all = k == 1 ? P.kind[0].N : 0;         // o waits for k and v too
+            if (k == 0 || k == 2) {
+                a.rscale = P.rnorm ? P.rnorm + 2 * l + (k >> 1) : nullptr;
+                a.cscale = ly.cs[k >> 1];
+            }
+            if (k == 1) gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
+            else if (k == 3) fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
+            else gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
+            __syncthreads();                             // the next phase reuses the LDS
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(P.calls + b, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
+    __shared__ __align__(16) ChainLds lds;
+    const ChainPlan& P = *plan;
+    if (P.fmt == OTPU_INT4) chain_run<OTPU_INT4>(P, lds);
+    else chain_run<OTPU_FP4>(P, lds);
+}
+
+static int64_t rnd256(int64_t x) { return (x + 255) / 256 * 256; }
+
+struct ChainLayout {
+    int64_t layer, calls, ll, rowb, total;
+};
+static ChainLayout chain_layout(int layers, int maxn) {
+    ChainLayout c;
+    c.layer = rnd256(sizeof(ChainPlan));
+    c.calls = c.layer + rnd256((int64_t)layers * sizeof(ChainLayer));
+    c.ll = c.calls + rnd256((int64_t)(CHAIN_SLOTS + 1) * 4);       // the call counters, then the error word
+    c.rowb = rnd256((int64_t)maxn * 8);
+    c.total = c.ll + 2 * c.rowb;
+    return c;
+}
+
+}  // namespace otpu
+
+using namespace otpu;
+
+extern "C" int64_t otpu_chain_plan_bytes(int layers, int hidden, int q_dim, int kv_dim, int F) {
+    if (layers < 1 || hidden < 1 || q_dim < 1 || kv_dim < 0 || F < 1) return -1;
+    const int maxn = std::max(std::max(q_dim + 2 * kv_dim, hidden), 2 * F);
+    return chain_layout(layers, maxn).total;
+}
+
+extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int fmt,
+                               const uint8_t* const* w, const int64_t* rs, const uint8_t* const* ws,
+                               const int64_t* srs, const float* rnorm, const float* const* cscale, const float* x,
+                               float* const* outs, void* plan, int64_t plan_bytes) {
+    if (fmt != OTPU_INT4 && fmt != OTPU_FP4) return otpu_fail(OTPU_EINVAL, "chain_plan: int4x or fp4x6 weights");
+    if (layers < 1 || !w || !rs || !ws || !srs || !x || !outs || !plan)
+        return otpu_fail(OTPU_EINVAL, "chain_plan: layers %d, NULL arrays", layers);
+    if (hidden > 32 * QKV_T || q_dim > 32 * O_T || F % 256 || F > 32 * DN_T * DN_L || q_dim % 32 || hidden % 32 ||
+        kv_dim < 0)
+        return otpu_fail(OTPU_EINVAL, "chain_plan: hidden %d (<= %d), q_dim %d (<= %d), F %d (a multiple of 256, <= %d)",
+                         hidden, 32 * QKV_T, q_dim, 32 * O_T, F, 32 * DN_T * DN_L);
+    if ((uintptr_t)plan % 256) return otpu_fail(OTPU_EALIGN, "chain_plan: plan 256-byte aligned");
+    const int nq = q_dim + 2 * kv_dim;
+    const int maxn = std::max(std::max(nq, hidden), 2 * F);
+    const ChainLayout lay = chain_layout(layers, maxn);
+    if (plan_bytes < lay.total)
+        return otpu_fail(OTPU_EINVAL, "chain_plan: %lld bytes, the plan needs %lld", (long long)plan_bytes,
+                         (long long)lay.total);
+    if (otpu_cu_count() > CHAIN_SLOTS) return otpu_fail(OTPU_EINVAL, "chain_plan: more than %d CUs", CHAIN_SLOTS);
+    // each phase kind checked and built as its one-launch entry point would (layer 0's
+    // pointers); then every layer's pointers checked the same way
+    const int Ns[4] = {nq, hidden, 2 * F, hidden}, Ks[4] = {hidden, q_dim, hidden, F};
+    std::vector<ChainLayer> ly(layers);
+    ChainPlan hp = {};
+    for (int l = 0; l < layers; ++l) {
+        for (int k = 0; k < 4; ++k) {
+            const int j = 4 * l + k;
+            if (!outs[j]) return otpu_fail(OTPU_EINVAL, "chain_plan: layer %d phase %d output NULL", l, k);
+            if ((uintptr_t)outs[j] % 16) return otpu_fail(OTPU_EALIGN, "chain_plan: outputs 16-byte aligned");
+            MMArgs a;
+            int L = 1, rc;
+            const float* cs = (k == 0 || k == 2) && cscale ? cscale[2 * l + (k >> 1)] : nullptr;
+            const float* rsc = (k == 0 || k == 2) && rnorm ? rnorm + 2 * l + (k >> 1) : nullptr;
+            if (k < 3)
+                rc = qin_args(&a, &L, x, nullptr, rsc, cs, 1, 0, Ks[k], Ks[k], w[j], rs[j], ws[j], srs[j], Ns[k], fmt, 0,
+                              0, outs[j], Ns[k], 0);
+            else
+                rc = fold_args(&a, &L, x, x, nullptr, nullptr, F, w[j], rs[j], ws[j], srs[j], hidden, fmt, 0, 0, outs[j]);
+            if (rc) return rc;
+            if (l > 0 && (rs[j] != rs[k] || srs[j] != srs[k]))
+                return otpu_fail(OTPU_EINVAL, "chain_plan: layer %d phase %d row strides differ from layer 0's", l, k);
+            if (l == 0) {
+                a.T = k == 0 ? QKV_T : k == 1 ? O_T : k == 2 ? GU_T : DN_T;
+                if (k == 3) a.ll_mul = F;
+                hp.kind[k] = a;
+            }
+            ly[l].w[k] = w[j];
+            ly[l].ws[k] = ws[j];
+            ly[l].out[k] = outs[j];
+            if (k == 0 || k == 2) ly[l].cs[k >> 1] = cs;
+        }
+    }
+    uint8_t* base = static_cast<uint8_t*>(plan);
+    hp.x0 = x;
+    hp.rnorm = rnorm;
+    hp.layer = reinterpret_cast<const ChainLayer*>(base + lay.layer);
+    hp.calls = reinterpret_cast<uint32_t*>(base + lay.calls);
+    hp.err = hp.calls + CHAIN_SLOTS;
+    hp.ll[0] = reinterpret_cast<uint64_t*>(base + lay.ll);
+    hp.ll[1] = reinterpret_cast<uint64_t*>(base + lay.ll + lay.rowb);
+    hp.layers = layers;
+    hp.fmt = fmt;
+    // synchronous copies: a plan is built once, outside any capture
+    hipError_t e = hipMemset(base, 0, (size_t)lay.total);
+    if (e == hipSuccess) e = hipMemcpy(base, &hp, sizeof(hp), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(base + lay.layer, ly.data(), sizeof(ChainLayer) * layers, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "chain_plan: %s", hipGetErrorString(e));
+    return OTPU_OK;
+}
+
+extern "C" int otpu_chain_step(const void* plan, otpu_stream_t stream) {
+    if (!plan || (uintptr_t)plan % 256) return otpu_fail(OTPU_EINVAL, "chain_step: plan NULL or misaligned");
+    // one workgroup a CU (the padding LDS leaves room for no second; without it the workgroups
+    // are resident all the same, some sharing a CU)
+    static const int pad = [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(chain_kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, CHAIN_PAD_LDS) == hipSuccess
+                   ? CHAIN_PAD_LDS : 0;
+    }();
+#ifndef OTPU_CHAIN_WGS
+#define OTPU_CHAIN_WGS 4096
+#endif
+    const int G = std::min(otpu_cu_count(), OTPU_CHAIN_WGS);
+    chain_kernel<<<(unsigned)G, 256, pad, (hipStream_t)stream>>>(static_cast<const ChainPlan*>(plan));
+    return otpu_launch_check("chain_step");
+}
+
+extern "C" int otpu_chain_error(const void* plan, uint32_t* err) {
+    if (!plan || !err) return otpu_fail(OTPU_EINVAL, "chain_error: NULL");
+    ChainPlan hp;
+    hipError_t e = hipMemcpy(&hp, plan, sizeof(hp), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(err, hp.err, 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "chain_error: %s", hipGetErrorString(e));
+    return OTPU_OK;
+}

@@ -263,10 +263,12 @@ extern "C" int otpu_mm_ranges(const int8_t* q, int64_t ldq, const float* Sa, con
     return otpu_launch_check("mm_ranges");
 }
 
-extern "C" int otpu_mm_qin(const float* x, const float* xmul, const float* rscale, const float* cscale, int nsum,
-                           int64_t sum_stride, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
-                           int64_t srs, int N, int fmt, int flags, int k0, float* out, int64_t ors, int64_t part_stride,
-                           otpu_stream_t stream) {
+namespace otpu {
+// the checks and the argument block of one otpu_mm_qin (pieces a lane in *L; also the persistent
+// chain's linears)
+int qin_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float* rscale, const float* cscale,
+             int nsum, int64_t sum_stride, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
+             int64_t srs, int N, int fmt, int flags, int k0, float* out, int64_t ors, int64_t part_stride) {
     const int chunk = fmt == OTPU_INT8 ? OTPU_D : 2 * OTPU_D;
     if (width < chunk || width % chunk || K % width || width > QIN_KMAX)
         return otpu_fail(OTPU_EINVAL, "mm_qin: ranges of %d over K %d (multiples of %d, at most %d)", width, K, chunk,
@@ -292,8 +294,22 @@ extern "C" int otpu_mm_qin(const float* x, const float* xmul, const float* rscal
     a.rscale = rscale; a.cscale = cscale;
     a.w_bs = fmt == OTPU_INT8 ? width : width / 2; a.k0_bs = plain ? 0 : width / OTPU_D;
     a.P = (fmt == OTPU_INT8 ? width : width / 2) / 16;
+    pick_team(a.P, &a.T, Lp);
+    *ap = a;
+    return OTPU_OK;
+}
+}  // namespace otpu
+
+extern "C" int otpu_mm_qin(const float* x, const float* xmul, const float* rscale, const float* cscale, int nsum,
+                           int64_t sum_stride, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
+                           int64_t srs, int N, int fmt, int flags, int k0, float* out, int64_t ors, int64_t part_stride,
+                           otpu_stream_t stream) {
+    MMArgs a;
     int L = 1;
-    pick_team(a.P, &a.T, &L);
+    const int rc = qin_args(&a, &L, x, xmul, rscale, cscale, nsum, sum_stride, K, width, w, rs, ws, srs, N, fmt, flags,
+                            k0, out, ors, part_stride);
+    if (rc) return rc;
+    const int R = K / width;
     hipStream_t s = (hipStream_t)stream;
     switch (fmt) {
         case OTPU_INT8: launch_qin_fmt<OTPU_INT8>(a, L, R, s); break;
@@ -306,11 +322,12 @@ extern "C" int otpu_mm_qin(const float* x, const float* xmul, const float* rscal
 
 namespace otpu {
 void launch_fold(const MMArgs& a, int fmt, int L, hipStream_t s);   // gemv_fold.hip
-}
 
-extern "C" int otpu_mm_qin_fold(const float* x, const float* xmul, const float* rscale, const float* cscale, int K,
-                                const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
-                                int k0, float* out, otpu_stream_t stream) {
+// the checks and the argument block of one otpu_mm_qin_fold (pieces a lane in *L; also the
+// persistent chain's down projections)
+int fold_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float* rscale, const float* cscale,
+              int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
+              float* out) {
     if (fmt == OTPU_INT8) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: 4-bit weights (F-chunks of 256)");
     if (flags & ~OTPU_PAIR) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: no flags (weights with scale rows)");
     if (K < 256 || K % 256 || K > QIN_KMAX)
@@ -330,6 +347,19 @@ extern "C" int otpu_mm_qin_fold(const float* x, const float* xmul, const float* 
     int L = 1;
     pick_team(a.P, &a.T, &L);
     if (L > 4) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: K %d needs %d pieces a lane (at most 4)", K, L);
+    *ap = a;
+    *Lp = L;
+    return OTPU_OK;
+}
+}  // namespace otpu
+
+extern "C" int otpu_mm_qin_fold(const float* x, const float* xmul, const float* rscale, const float* cscale, int K,
+                                const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
+                                int k0, float* out, otpu_stream_t stream) {
+    MMArgs a;
+    int L = 1;
+    const int rc = fold_args(&a, &L, x, xmul, rscale, cscale, K, w, rs, ws, srs, N, fmt, flags, k0, out);
+    if (rc) return rc;
     launch_fold(a, fmt, L, (hipStream_t)stream);
     return otpu_launch_check("mm_qin_fold");
 }

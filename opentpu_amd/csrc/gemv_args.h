@@ -36,6 +36,16 @@ struct MMArgs {
     const float* cscale;
     int nsum;
     int64_t sum_stride, xin_bs;
+    // the persistent chain's hand-off rows (LL kernels only): 8-byte entries tag << 32 | fp32
+    // bits, written with device-scope stores and polled with device-scope loads until every
+    // entry a workgroup needs carries the phase's tag (no fences, no counters)
+    const uint64_t* ll_in;         // input entries (NULL: the plain row xin); xmul's at ll_in + ll_mul
+    uint64_t* ll_out;              // output entries, besides the plain row out
+    int64_t ll_mul;
+    uint32_t tag_in, tag_out;
+    uint32_t* err;                 // set when a wait runs out of polls
+    int spin;                      // polls a wait allows (~1 us each)
+    int ll_all;                    // entries of the input row to wait for when more than K (see ll_drain)
 };
 
 constexpr int QIN_KMAX = 4096;     // columns a prologue QACT holds in LDS

@@ -165,6 +165,101 @@ __device__ __forceinline__ double xsum(double x, int o) {
     return x + (o == 8 ? dpp_partner<8>(x) : o == 4 ? dpp_partner<4>(x) : o == 2 ? dpp_partner<2>(x) : dpp_partner<1>(x));
 }
 
+// ---- the persistent chain's hand-off entries (LL kernels) ----
+#ifndef OTPU_LL_SLEEP
+#define OTPU_LL_SLEEP 1                          // s_sleep between polls (64 clocks a unit)
+#endif
+__device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_store(uint64_t* p, uint32_t tag, float y) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | fbits(y), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// this thread's float4 chunks c = tid + 256 k (k < CPT, c < NC) of the entry row a.ll_in, and
+// with MUL of the row a.ll_in + a.ll_mul: every entry is loaded at once, then the entries that
+// do not carry a.tag_in yet are loaded again until they do.  A wait that runs out of polls sets
+// *a.err and goes on with what it has (the step's output is then invalid; every wave still ends).
+template <int CPT, bool MUL>
+__device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[CPT], float4 (&gv)[CPT]) {
+    constexpr int NR = MUL ? 2 : 1;
+    const int tid = threadIdx.x;
+    uint64_t e[NR][CPT][4];
+#pragma unroll
+    for (int h = 0; h < NR; ++h)
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int c = tid + 256 * k;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                e[h][k][j] = c < NC ? ll_load(a.ll_in + (h ? a.ll_mul : 0) + 4 * c + j) : (uint64_t)a.tag_in << 32;
+        }
+    for (int n = 0;; ++n) {
+        bool done = true;
+#pragma unroll
+        for (int h = 0; h < NR; ++h)
+#pragma unroll
+            for (int k = 0; k < CPT; ++k)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if ((uint32_t)(e[h][k][j] >> 32) != a.tag_in) {
+                        done = false;
+                        e[h][k][j] = ll_load(a.ll_in + (h ? a.ll_mul : 0) + 4 * (tid + 256 * k) + j);
+                    }
+        if (done) break;
+        if (n >= a.spin) {
+            __hip_atomic_fetch_or(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
+    }
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        xv[k] = make_float4(bitsf((uint32_t)e[0][k][0]), bitsf((uint32_t)e[0][k][1]), bitsf((uint32_t)e[0][k][2]),
+                            bitsf((uint32_t)e[0][k][3]));
+        if (MUL)
+            gv[k] = make_float4(bitsf((uint32_t)e[NR - 1][k][0]), bitsf((uint32_t)e[NR - 1][k][1]),
+                                bitsf((uint32_t)e[NR - 1][k][2]), bitsf((uint32_t)e[NR - 1][k][3]));
+    }
+}
+
+// wait for entries [from, to) of the input row as well, values unused: a phase that reads part of
+// its input row (o reads q of q, k, v) still waits for every producer of that row, so every
+// workgroup that wrote into it has finished reading the row before (which the alternating
+// entry rows rely on)
+__device__ __forceinline__ void ll_drain(const MMArgs& a, int from, int to) {
+    constexpr int NE = 8;                                // entries a thread at most (to - from <= 2048)
+    const int tid = threadIdx.x;
+    uint64_t e[NE];
+#pragma unroll
+    for (int j = 0; j < NE; ++j) {
+        const int i = from + tid + 256 * j;
+        e[j] = i < to ? ll_load(a.ll_in + i) : (uint64_t)a.tag_in << 32;
+    }
+    for (int n = 0;; ++n) {
+        bool done = true;
+#pragma unroll
+        for (int j = 0; j < NE; ++j)
+            if ((uint32_t)(e[j] >> 32) != a.tag_in) {
+                done = false;
+                e[j] = ll_load(a.ll_in + from + tid + 256 * j);
+            }
+        if (done) break;
+        if (n >= a.spin) {
+            __hip_atomic_fetch_or(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
+    }
+}
+
+// the prologue QACT's LDS: the quantized row, its group offsets, the waves' maxima
+struct QinLds {
+    uint32_t qs[QIN_KMAX / 4];
+    uint8_t ds[QIN_KMAX / 32];
+    uint32_t red[4];
+};
+
 // QACT of the problem's fp32 row in the prologue (fp32.quantize_mx(x, 32) of one row, as
 // qact_kernel computes it), once per workgroup: each thread takes float4 chunks of the row
 // (folding nsum partial rows in order, times xmul when given, then QACT's RSCALE and CSCALE
@@ -177,12 +272,23 @@ __device__ __forceinline__ double xsum(double x, int o) {
 // waits for the row only, while the weights stream in (c4: 724 -> 659 us a step).  With a fold
 // (nsum > 1) the weights go first and the fold's loads after them (the other order measured
 // the same).
-template <int FMT, int L, int T, typename IssueWeights>
+// LL (the persistent chain): the row comes from hand-off entries when a.ll_in is set (the
+// weights and scale factors go out first: they do not wait for the hand-off), and the LDS is
+// the caller's (one block for all of the kernel's phases).
+template <int FMT, int L, int T, bool LL = false, typename IssueWeights>
 __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&act)[L][FMT == OTPU_INT8 ? 4 : 8],
-                                             int (&shA)[L], float& sa2, IssueWeights&& issue_weights) {
-    __shared__ __align__(16) uint32_t qs[QIN_KMAX / 4];
-    __shared__ uint8_t ds[QIN_KMAX / 32];
-    __shared__ uint32_t red[4];
+                                             int (&shA)[L], float& sa2, IssueWeights&& issue_weights,
+                                             QinLds* lds = nullptr) {
+    QinLds* S;
+    if constexpr (LL) {
+        S = lds;
+    } else {
+        __shared__ __align__(16) QinLds own;
+        S = &own;
+    }
+    uint32_t* qs = S->qs;
+    uint8_t* ds = S->ds;
+    uint32_t* red = S->red;
     // float4 chunks a thread holds at most: the row has at most L T pieces of 16 (int8) or 32
     // (4-bit) elements, so for the small rows of a chain only the chunks that can exist are
     // compiled (the code runs once per launch, from a cold instruction cache)
@@ -218,6 +324,14 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
     };
     if (a.nsum == 1) {
         float4 xv[CPT], gv[CPT];
+        if (LL && a.ll_in) {                             // (no VOP MUL in the chain's linears)
+            load_scales();
+            __builtin_amdgcn_sched_barrier(0);
+            issue_weights();
+            __builtin_amdgcn_sched_barrier(0);
+            ll_chunks<CPT, false>(a, NC, xv, gv);
+            if (a.ll_all > K) ll_drain(a, K, a.ll_all);
+        } else {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
             const int c = tid + 256 * k;
@@ -230,6 +344,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
         __builtin_amdgcn_sched_barrier(0);
         issue_weights();
         __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
             const int c = tid + 256 * k;
@@ -325,9 +440,10 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
 }
 
 // the kernel body for a team of T lanes (T a compile-time constant: the exchanges of the
-// reduction are then straight-line code); QIN: the activation row is quantized in the prologue
-template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN, int R>
-__device__ __forceinline__ void gemv_body(const MMArgs& a) {
+// reduction are then straight-line code); QIN: the activation row is quantized in the prologue;
+// LL: a phase of the persistent chain (hand-off entries in and out, the caller's LDS)
+template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN, int R, bool LL = false>
+__device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr) {
     constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
     constexpr int E = R * MR;                             // sums a lane carries per iteration
     static_assert(E <= T, "a team holds its E sums after the reduce-scatter");
@@ -465,6 +581,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a) {
                 float y = fmul_f(fmul_f((float)tot, st.sw), sa2[ej]);
                 if constexpr (QIN) {                  // (no ACC / ASCALE / RMAX / LM head here)
                     out[(int64_t)ej * a.ors + n] = y;
+                    if constexpr (LL) ll_store(a.ll_out + n, a.tag_out, y);
                     return;
                 }
                 if (out) {
@@ -489,9 +606,9 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a) {
         // the first rows stream in while the workgroup quantizes the activation row
         Stage st;
         const int nfirst = wave * RW;
-        qin_prologue<FMT, L, T>(a, b, act[0], shA[0], sa2[0], [&] {
+        qin_prologue<FMT, L, T, LL>(a, b, act[0], shA[0], sa2[0], [&] {
             if (nfirst < a.N) load(st, nfirst);
-        });
+        }, lds);
         for (int n0 = nfirst; n0 < a.N; n0 += stride) {
             if (n0 != nfirst) load(st, n0);
             compute(st, n0);

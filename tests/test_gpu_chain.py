@@ -231,8 +231,16 @@ def test_chain_layers_small(X):
     ch.fused = False
     assert same_bits(ch.step(x).cpu().numpy(), want)
     ch.fused = True
-    assert ch.fold
+    assert ch.fold and ch.persistent and ch.kernels_per_step == 1
+    say("chain small: persistent step")
     assert same_bits(ch.step(x).cpu().numpy(), want)
+    # every phase's plain output row: the last layer's
+    assert same_bits(ch.gu.cpu().numpy(), CH.layer(CH.step(x, host[:2], "int4", 512, 768), host[2], "int4", 512,
+                                                   768)[1]["gu"])
+    assert ch.chain_error() == 0
+    ch.persistent = False
+    assert same_bits(ch.step(x).cpu().numpy(), want)
+    ch.persistent = True
     ch.fold = False                                # the down chunks' partial rows, folded later
     assert same_bits(ch.step(x).cpu().numpy(), want)
     ch.fold = True
@@ -261,15 +269,18 @@ def test_chain_with_norms(X):
     x = rng.standard_normal((1, 256)).astype(np.float32)
     want = CH.step(x, host, "int4", 512, 768, onorms)
     assert not same_bits(want, CH.step(x, host, "int4", 512, 768))
-    for fused, fold in ((True, True), (True, False), (False, True)):
-        ch.fused, ch.fold = fused, fold
-        say("chain with norms", fused, fold)
-        assert same_bits(ch.step(x).cpu().numpy(), want), (fused, fold)
+    for fused, fold, pers in ((True, True, True), (True, True, False), (True, False, False), (False, True, False)):
+        ch.fused, ch.fold, ch.persistent = fused, fold, pers
+        say("chain with norms", fused, fold, pers)
+        assert same_bits(ch.step(x).cpu().numpy(), want), (fused, fold, pers)
     ch.fused, ch.fold = True, True
-    ch.capture()
-    for i in range(2):
-        assert same_bits(ch.replay(x).cpu().numpy(), want), f"replay {i}"
-        torch.cuda.synchronize()
+    for pers in (True, False):
+        ch.persistent = pers
+        ch.capture()
+        for i in range(2):
+            assert same_bits(ch.replay(x).cpu().numpy(), want), f"replay {i} persistent {pers}"
+            torch.cuda.synchronize()
+    assert ch.chain_error() == 0
 
 
 def test_chain_c4_full_and_graph(X):
@@ -296,8 +307,12 @@ def test_chain_c4_full_and_graph(X):
     say("nonzero outputs per layer", nonzero)
     assert nonzero[0] > 900
     want = xo
-    say("chain c4: eager step, fused (folded down projection, and partial rows) and unfused")
-    assert ch.fold and ch.kernels_per_step == 112
+    say("chain c4: eager step, persistent, fused (folded down projection, and partial rows) and unfused")
+    assert ch.fold and ch.persistent and ch.kernels_per_step == 1
+    assert same_bits(ch.step(x).cpu().numpy(), want)
+    assert ch.chain_error() == 0
+    ch.persistent = False
+    assert ch.kernels_per_step == 112
     assert same_bits(ch.step(x).cpu().numpy(), want)
     ch.fold = False
     assert same_bits(ch.step(x).cpu().numpy(), want)
@@ -316,15 +331,18 @@ def test_chain_c4_full_and_graph(X):
         assert same_bits(yl.cpu().numpy(), want_l), f"fused layer {l}"
         ch.layer_folded(l, ch.x, yl)
         assert same_bits(yl.cpu().numpy(), want_l), f"folded layer {l}"
-    say("chain c4: graph")
-    ch.capture()
-    for i in range(3):
-        xi = rng.standard_normal((1, 1024)).astype(np.float32) if i == 1 else x
-        got = ch.replay(xi).cpu().numpy()
-        exp = want if i != 1 else CH.step(xi, host, "int4")
-        assert same_bits(got, exp), f"replay {i}"
-        torch.cuda.synchronize()
-        ch.qkv.fill_(float(i))                     # eager work between replays
+    x1 = rng.standard_normal((1, 1024)).astype(np.float32)
+    want1 = CH.step(x1, host, "int4")
+    for pers in (False, True):
+        say("chain c4: graph, persistent", pers)
+        ch.persistent = pers
+        ch.capture()
+        for i in range(3):
+            got = ch.replay(x1 if i == 1 else x).cpu().numpy()
+            assert same_bits(got, want1 if i == 1 else want), f"replay {i} persistent {pers}"
+            torch.cuda.synchronize()
+            ch.qkv.fill_(float(i))                 # eager work between replays
+    assert ch.chain_error() == 0
 
 
 def test_chain_c4_layers_against_the_float64_emulation(X):
@@ -350,3 +368,52 @@ def test_chain_c4_layers_against_the_float64_emulation(X):
         for k, g in got.items():
             err = np.abs(g.astype(np.float64) - me[k]).max()
             assert err <= EMU_TOL * np.abs(me[k]).max(), (l, k, err / np.abs(me[k]).max())
+
+
+@pytest.mark.parametrize("fmt", ["fp4", "int4"])
+def test_chain_persistent_formats_and_shapes(X, fmt):
+    """The persistent step (otpu_chain_step) on fp4x6 and int4x weights at a shape whose phases
+    leave most workgroups without rows (hidden 512, q_dim 1024, F 1536, 4 layers, norms): the
+    oracle's step bit for bit, eager and over graph replays with new inputs, the error word 0."""
+    import torch
+    from opentpu_amd.chain import DecodeChain, Shape
+    sh = Shape(hidden=512, q_dim=1024, kv_dim=256, F=1536, layers=4)
+    say("chain persistent", fmt)
+    base = DecodeChain.synthetic(sh, fmt, seed0=21, std=0.04)
+    rng = np.random.default_rng(22)
+    norms = [(rng.uniform(0.5, 2.0, 512).astype(np.float32), rng.uniform(0.5, 2.0, 512).astype(np.float32))
+             for _ in range(sh.layers)]
+    ch = DecodeChain(base.layers, sh, fmt, True, norms)
+    assert ch.persistent
+    r = rng.uniform(0.5, 3.0, (sh.layers, 2)).astype(np.float32)
+    ch.rnorm.copy_(torch.from_numpy(r).cuda())
+    host = _host_layers(ch)
+    onorms = [(norms[l][0], norms[l][1], r[l, 0:1], r[l, 1:2]) for l in range(sh.layers)]
+    xs = [rng.standard_normal((1, 512)).astype(np.float32) for _ in range(3)]
+    wants = [CH.step(x, host, fmt, 1024, 1536, onorms) for x in xs]
+    assert same_bits(ch.step(xs[0]).cpu().numpy(), wants[0])
+    ch.capture()
+    for i in range(4):
+        assert same_bits(ch.replay(xs[i % 3]).cpu().numpy(), wants[i % 3]), f"replay {i}"
+        torch.cuda.synchronize()
+    assert same_bits(ch.step(xs[2]).cpu().numpy(), wants[2])
+    assert ch.chain_error() == 0
+
+
+def test_chain_plan_refusals(X):
+    """otpu_chain_plan refuses what its compiled phases cannot hold, before touching the plan."""
+    import ctypes as C
+    import torch
+    from opentpu_amd._lib import OtpuError
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    P4 = C.c_void_p * 4
+    I4 = C.c_int64 * 4
+    p = X.ptr(buf)
+    arr = P4(p, p, p, p)
+    for layers, hidden, q, kv, F, fmt in ((1, 2048, 2048, 512, 3072, 1), (1, 1024, 4096, 512, 3072, 1),
+                                         (1, 1024, 2048, 512, 3200, 1), (1, 1024, 2048, 512, 3072, 0),
+                                         (1, 1024, 2048, 512, 6144, 2), (0, 1024, 2048, 512, 3072, 1)):
+        with pytest.raises(OtpuError):
+            X.call("otpu_chain_plan", layers, hidden, q, kv, F, fmt, arr, I4(512, 1024, 512, 1536), arr,
+                   I4(64, 128, 64, 192), None, None, p, arr, p, 1 << 20)
+    assert X.load().otpu_chain_plan_bytes(0, 1024, 2048, 512, 3072) == -1
