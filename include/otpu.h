@@ -191,7 +191,7 @@ int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float
  *   [layers, 2] (device) or NULL; cscale: 2 a layer (gamma of the qkv and the gate/up QACTs,
  *   device, entries may be NULL) or NULL; x: the step's input row [hidden]; outs: the phases' fp32
  *   output rows (qkv [q_dim + 2 kv_dim], o [hidden], gu [2 F], down [hidden]).  int4x or fp4x6
- *   weights; hidden <= 1024, q_dim <= 2048, F a multiple of 256 and <= 3072, hidden and q_dim
+ *   weights; hidden <= 1024, q_dim <= 2048, F a multiple of 256 and <= 4096, hidden and q_dim
  *   multiples of 32.
  *   otpu_chain_step: one step (reads x, writes every output row); capturable in a HIP graph.
  *   otpu_chain_error: the plan's error word (0: every hand-off completed; 1: a wait ran out of
@@ -203,6 +203,11 @@ int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int fm
                     int64_t plan_bytes);
 int otpu_chain_step(const void* plan, otpu_stream_t stream);
 int otpu_chain_error(const void* plan, uint32_t* err);
+/* Profiling: clock stamps of every phase and workgroup into stamps [4 layers][grid][8] (uint64,
+ * the 100 MHz clock: phase start, weights issued, input row in, QACT done, rows stored; NULL
+ * stops).  Only a library built with the stamps (python -m opentpu_amd.build --stamps); others
+ * refuse (OTPU_EINVAL).  Synchronous. */
+int otpu_chain_stamps(void* plan, uint64_t* stamps);
 
 /* B independent MMs of one shape in one launch (a layer stack's or an expert set's decode
  * GEMVs): problem b's operands start at the given pointers plus b times the *_bstride

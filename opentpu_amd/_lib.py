@@ -45,6 +45,7 @@ SIGNATURES = {
     "otpu_chain_plan": ([_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L], _I),
     "otpu_chain_step": ([_P, _P], _I),
     "otpu_chain_error": ([_P, _P], _I),
+    "otpu_chain_stamps": ([_P, _P], _I),
     "otpu_ungroup_rows": ([_P, _I, _I, _I, _I, _I, _L, _P, _L, _P], _I),
     "otpu_ungroup_scales": ([_P, _I, _I, _I, _I, _I, _I, _P, _L, _P], _I),
     "otpu_import_mxfp4": ([_P, _L, _P, _L, _I, _I, _I, _P, _L, _P, _L, _P, _P], _I),

@@ -36,16 +36,22 @@ def _stale(src: str, obj: str) -> bool:
     return any(os.path.getmtime(d) > t for d in deps)
 
 
-def build(verbose: bool = True, incremental: bool = False) -> str:
+STAMPS_LIB = os.path.join(HERE, "libotpu_amd_stamps.so")
+
+
+def build(verbose: bool = True, incremental: bool = False, stamps: bool = False) -> str:
     """Compile every source to an object in parallel (one hipcc per file), then link.
     incremental: keep the objects in csrc/_build and recompile only those older than their
-    source or a header (a developer's loop; the default compiles everything)."""
+    source or a header (a developer's loop; the default compiles everything).
+    stamps: the profiling build, libotpu_amd_stamps.so, with the persistent chain's phase clock
+    stamps compiled in (OTPU_PHASE_STAMPS; read by python -m opentpu_amd.phases)."""
     import tempfile
     from concurrent.futures import ThreadPoolExecutor
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     inc = ["-I", os.path.join(HERE, "..", "include")]
-    cflags = [f for f in FLAGS if f != "-shared"]
-    keep = os.path.join(CSRC, "_build")
+    cflags = [f for f in FLAGS if f != "-shared"] + (["-DOTPU_PHASE_STAMPS"] if stamps else [])
+    lib = STAMPS_LIB if stamps else LIB
+    keep = os.path.join(CSRC, "_build_stamps" if stamps else "_build")
     if incremental:
         os.makedirs(keep, exist_ok=True)
     with tempfile.TemporaryDirectory(prefix="otpu_build_") as tmpd:
@@ -65,7 +71,7 @@ def build(verbose: bool = True, incremental: bool = False) -> str:
                 sys.stderr.write(r.stdout + r.stderr)
                 raise RuntimeError(f"hipcc failed on {obj}")
             warn += [l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip()]
-        tmp = LIB + ".tmp"
+        tmp = lib + ".tmp"
         cmd = [hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *[o for o, _ in results], "-o", tmp]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
@@ -73,9 +79,9 @@ def build(verbose: bool = True, incremental: bool = False) -> str:
             raise RuntimeError("link failed")
     if verbose and warn:
         print("\n".join(warn))
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    build(incremental="--incremental" in sys.argv)
+    build(incremental="--incremental" in sys.argv, stamps="--stamps" in sys.argv)

@@ -62,7 +62,7 @@ class DecodeChain:
     """`layers`: per layer a dict name -> (rows, srows) device tensors (uint8).
 
     persistent (default where it applies: fused and folded, int4 / fp4 weights, hidden <= 1024,
-    q_dim <= 2048, F <= 3072): the whole step is one launch of otpu_chain_step, its phases handing
+    q_dim <= 2048, F <= 4096): the whole step is one launch of otpu_chain_step, its phases handing
     rows to each other on the GPU; the same bits as the four kernels a layer below.
     fused: a layer is four kernels, each linear an otpu_mm_qin (the QACT of its input
     row in the GEMV's prologue).  With 4-bit weights and 256-column down chunks the down
@@ -118,7 +118,7 @@ class DecodeChain:
         self.persistent = self.persistent_fits() if persistent is None else bool(persistent)
         if self.persistent and not self.persistent_fits():
             raise ValueError("DecodeChain: the persistent step needs fused, folded int4 / fp4 layers with "
-                             "hidden <= 1024, q_dim <= 2048, F <= 3072")
+                             "hidden <= 1024, q_dim <= 2048, F <= 4096")
 
     @staticmethod
     def synthetic(shape: Shape = Shape(), fmt: str = "int4", seed0: int = 100, std: float = 0.02,
@@ -219,7 +219,7 @@ class DecodeChain:
         """Whether otpu_chain_step can run this chain (its phases' teams are compiled in)."""
         s = self.shape
         return (self.fused and self.fold and self.fmt in ("int4", "fp4") and s.hidden <= 1024 and s.hidden % 32 == 0
-                and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 3072 and s.F % 256 == 0)
+                and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 4096 and s.F % 256 == 0)
 
     def _use_persistent(self) -> bool:
         return self.persistent and self.fused and self.fold

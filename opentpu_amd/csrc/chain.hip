@@ -22,8 +22,9 @@
 // of polls sets the plan's error word and the step goes on (its output is then invalid).
 //
 // Phases' teams (compile-time): qkv and gate/up 32 lanes a row (K <= 1024), o 64 lanes
-// (K <= 2048), the down projection 32 lanes with 3 pieces each (F <= 3072, F-chunks of 256).
+// (K <= 2048), the down projection 64 lanes with 2 pieces each (F <= 4096, F-chunks of 256).
 #include <algorithm>
+#include <cstddef>
 #include <vector>
 
 #include "gemv_fold.h"
@@ -51,7 +52,12 @@ constexpr int QKV_T = 32, QKV_R = OTPU_CHAIN_R; // (the gate/up phase's body too
 #endif
 constexpr int O_T = 64, O_R = OTPU_CHAIN_OR;
 constexpr int GU_T = QKV_T, GU_R = QKV_R;
-constexpr int DN_T = 32, DN_L = 3;
+// the fold: 64 lanes a row (1024 rows on 256 workgroups; 32 lanes with 128 workgroups measured
+// 526 against 519 us a step)
+#ifndef OTPU_CHAIN_DNT
+#define OTPU_CHAIN_DNT 64
+#endif
+constexpr int DN_T = OTPU_CHAIN_DNT, DN_L = 128 / DN_T;  // F <= 4096: 128 pieces a row
 
 struct ChainLayer {                              // the pointers of one layer (qkv, o, gu, down)
     const uint8_t* w[4];
@@ -69,6 +75,7 @@ struct ChainPlan {                               // device memory: the header, t
     uint32_t* calls;                             // call counter per workgroup
     uint32_t* err;
     int layers, fmt;
+    uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
 };
 
 // rows of phase kind k the first iteration of workgroup b covers start at b * rows_per_wg(k)
@@ -93,6 +100,10 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * l + k;
             MMArgs a = P.kind[k];
+            // stamps: 0 phase start, 1 weights issued (the wait starts), 2 input row in, 3 QACT
+            // done, 4 rows stored
+            a.stamp = P.stamps ? P.stamps + ((int64_t)i * gridDim.x + b) * 8 : nullptr;
+            OTPU_STAMP(a, 0);
             if (b * rows_per_wg(k) >= a.N) continue;     // no rows here: nothing to wait for
             a.w = ly.w[k];
             a.ws = ly.ws[k];
@@ -112,6 +123,7 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             if (k == 1) gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
             else if (k == 3) fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
             else gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
+            OTPU_STAMP(a, 4);
             __syncthreads();                             // the next phase reuses the LDS
         }
     }
@@ -235,6 +247,20 @@ extern "C" int otpu_chain_step(const void* plan, otpu_stream_t stream) {
     const int G = std::min(otpu_cu_count(), OTPU_CHAIN_WGS);
     chain_kernel<<<(unsigned)G, 256, pad, (hipStream_t)stream>>>(static_cast<const ChainPlan*>(plan));
     return otpu_launch_check("chain_step");
+}
+
+extern "C" int otpu_chain_stamps(void* plan, uint64_t* stamps) {
+#ifdef OTPU_PHASE_STAMPS
+    if (!plan) return otpu_fail(OTPU_EINVAL, "chain_stamps: plan NULL");
+    hipError_t e = hipMemcpy(static_cast<uint8_t*>(plan) + offsetof(ChainPlan, stamps), &stamps, sizeof(stamps),
+                             hipMemcpyHostToDevice);
+    if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "chain_stamps: %s", hipGetErrorString(e));
+    return OTPU_OK;
+#else
+    (void)plan;
+    (void)stamps;
+    return otpu_fail(OTPU_EINVAL, "chain_stamps: a build without phase stamps (python -m opentpu_amd.build --stamps)");
+#endif
 }
 
 extern "C" int otpu_chain_error(const void* plan, uint32_t* err) {

@@ -46,7 +46,21 @@ struct MMArgs {
     uint32_t* err;                 // set when a wait runs out of polls
     int spin;                      // polls a wait allows (~1 us each)
     int ll_all;                    // entries of the input row to wait for when more than K (see ll_drain)
+    uint64_t* stamp;               // the phase's clock stamps (builds with OTPU_PHASE_STAMPS only)
 };
+
+// a clock stamp (100 MHz wall clock) of the persistent chain's phase breakdown, by the first
+// thread, compiled only into the stamped build (python -m opentpu_amd.build --stamps)
+#ifdef OTPU_PHASE_STAMPS
+#define OTPU_STAMP(a, j)                                                                           \
+    do {                                                                                           \
+        if ((a).stamp && threadIdx.x == 0) (a).stamp[j] = __builtin_amdgcn_s_memrealtime();        \
+    } while (0)
+#else
+#define OTPU_STAMP(a, j) \
+    do {                 \
+    } while (0)
+#endif
 
 constexpr int QIN_KMAX = 4096;     // columns a prologue QACT holds in LDS
 constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds

@@ -106,7 +106,8 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
             st.wv[i] = ld16(wr + 16 * pc);
             st.sc[i] = piece_scale<FMT>(sr, 0u, a.k0, pc, false);
         }
-        st.sw = ftz(*reinterpret_cast<const float*>(sr));
+        const float swr = *reinterpret_cast<const float*>(sr);
+        st.sw = LL ? swr : ftz(swr);                    // (LL: flushed where used, as in gemv_body)
     };
 
     // 1. the input row's loads, then the first row's weights (loads complete in order); LL:
@@ -124,7 +125,9 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
         }
         if (wave * NT < a.N) load(st, nfirst);
         __builtin_amdgcn_sched_barrier(0);
+        OTPU_STAMP(a, 1);
         ll_chunks<CPT, true>(a, NC, xv, gv);
+        OTPU_STAMP(a, 2);
     } else {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -214,6 +217,7 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
         sa2[i] = ok ? sa2s[p / FOLD_PPR] : 0.0f;
     }
 
+    if constexpr (LL) OTPU_STAMP(a, 3);
     // 4. rows: per range the exact sum over its 8 lanes, its epilogue, the fold in range order
     for (int n0 = wave * NT; n0 < a.N; n0 += nwaves * NT) {
         const int n = n0 + team;
@@ -229,7 +233,7 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
             s = xsum(s, 4);
             // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw and
             // the finished Sa * 2^-W need no operand flush
-            yr[i] = fmul_f(fmul_f((float)s, st.sw), sa2[i]);
+            yr[i] = fmul_f(fmul_f((float)s, LL ? ftz(st.sw) : st.sw), sa2[i]);
         }
         // the team's first lane gathers the ranges' outputs (lanes team T + 8 g of slot i hold
         // range i GPT + g) and adds them in range order; the outputs are fmul results, flushed

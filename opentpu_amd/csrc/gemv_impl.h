@@ -329,8 +329,10 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
             __builtin_amdgcn_sched_barrier(0);
             issue_weights();
             __builtin_amdgcn_sched_barrier(0);
+            OTPU_STAMP(a, 1);
             ll_chunks<CPT, false>(a, NC, xv, gv);
             if (a.ll_all > K) ll_drain(a, K, a.ll_all);
+            OTPU_STAMP(a, 2);
         } else {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
@@ -541,7 +543,10 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
                 st.sc[r][i] = piece_scale<FMT>(sb, soff, k0, pc, plain);
             }
         }
-        st.sw = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(sb + (uint32_t)min(er * NT + team, last) * (uint32_t)a.srs));
+        // (LL: flushed where it is used, so that issuing the loads waits for none of them and the
+        // hand-off's polls go out at once)
+        const float swr = unit ? 1.0f : *reinterpret_cast<const float*>(sb + (uint32_t)min(er * NT + team, last) * (uint32_t)a.srs);
+        st.sw = LL ? swr : ftz(swr);
     };
     auto compute = [&](const Stage& st, int n0) {
         double v[E];
@@ -578,7 +583,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             } else {
                 // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw
                 // and the finished Sa * 2^-W need no operand flush
-                float y = fmul_f(fmul_f((float)tot, st.sw), sa2[ej]);
+                float y = fmul_f(fmul_f((float)tot, LL ? ftz(st.sw) : st.sw), sa2[ej]);
                 if constexpr (QIN) {                  // (no ACC / ASCALE / RMAX / LM head here)
                     out[(int64_t)ej * a.ors + n] = y;
                     if constexpr (LL) ll_store(a.ll_out + n, a.tag_out, y);
@@ -609,6 +614,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         qin_prologue<FMT, L, T, LL>(a, b, act[0], shA[0], sa2[0], [&] {
             if (nfirst < a.N) load(st, nfirst);
         }, lds);
+        if constexpr (LL) OTPU_STAMP(a, 3);
         for (int n0 = nfirst; n0 < a.N; n0 += stride) {
             if (n0 != nfirst) load(st, n0);
             compute(st, n0);

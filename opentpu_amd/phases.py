@@ -1,0 +1,87 @@
+"""Phase breakdown of the persistent chained decode step (the c4 workload: 28 Qwen3-0.6B-shaped
+layers of int4x linears) from per-workgroup clock stamps.
+
+    python -m opentpu_amd.build --stamps      # libotpu_amd_stamps.so: the stamps compiled in
+    python -m opentpu_amd.phases              # on a GPU: the table below
+
+Each workgroup stamps the 100 MHz wall clock at five points of every phase it has rows in:
+phase start, weights issued (its wait for the input row starts), input row in (every entry
+carries the phase's tag), QACT done (the activation pieces in registers), rows stored.  Per
+linear (medians over workgroups, means over the 28 layers) the table gives those four
+intervals, the hand-off (the previous phase's last workgroup done -> this phase's median
+workgroup with its input in: store visibility plus polling), and the tail (median -> last
+workgroup done).  Two weight copies alternate, as in bench.py; the step is replayed from a HIP
+graph.  Measurement only: the stamped library is not the product's."""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+NAMES = ("qkv", "o", "gate/up", "down (fold)")
+TICK_NS = 10.0                                  # s_memrealtime: 100 MHz
+
+
+def breakdown(st: np.ndarray) -> dict:
+    """st [phases, grid, 8] stamps -> per linear kind: the mean over layers of the medians (us)."""
+    rows = {n: [] for n in NAMES}
+    prev_end = None
+    for i in range(st.shape[0]):
+        ran = st[i, :, 4] > 0
+        a = st[i][ran].astype(np.float64)
+        if not len(a):
+            continue
+        end = a[:, 4].max()
+        if i > 0:                                # layer 0's qkv reads the plain input row
+            med = lambda j, k: np.median(a[:, k] - a[:, j]) * TICK_NS / 1e3
+            rows[NAMES[i % 4]].append([med(0, 1), med(1, 2), med(2, 3), med(3, 4),
+                                       (np.median(a[:, 2]) - prev_end) * TICK_NS / 1e3,
+                                       (end - np.median(a[:, 4])) * TICK_NS / 1e3, int(ran.sum())])
+        prev_end = end
+    return {n: np.mean(np.array(v), axis=0) for n, v in rows.items() if v}
+
+
+def main() -> None:
+    lib_path = os.path.join(HERE, "libotpu_amd_stamps.so")
+    if not os.path.exists(lib_path):
+        sys.exit("opentpu_amd.phases: build the stamped library first (python -m opentpu_amd.build --stamps)")
+    os.environ["OTPU_LIB"] = lib_path
+    import ctypes as C
+
+    import torch
+
+    from . import _lib as X
+    from .chain import DecodeChain, Shape
+    X.load(lib_path)
+    sh = Shape()
+    chains = [DecodeChain.synthetic(sh, "int4", seed0=100) for _ in range(2)]
+    x = torch.randn((1, sh.hidden), generator=torch.Generator(device="cuda").manual_seed(4), device="cuda")
+    for c in chains:
+        c.x.copy_(x)
+        c.capture()
+    torch.cuda.synchronize()
+    G = torch.cuda.get_device_properties(0).multi_processor_count
+    st = torch.zeros((4 * sh.layers, G, 8), dtype=torch.int64, device="cuda")
+    X.call("otpu_chain_stamps", C.c_void_p(chains[0]._plan_ptr()), C.c_void_p(st.data_ptr()))
+    for _ in range(3):                              # steps alternating between the two copies
+        chains[1]._graph.replay()
+        chains[0]._graph.replay()
+    torch.cuda.synchronize()
+    X.call("otpu_chain_stamps", C.c_void_p(chains[0]._plan_ptr()), None)
+    s = st.cpu().numpy()
+    if chains[0].chain_error():
+        sys.exit("opentpu_amd.phases: a hand-off wait ran out of polls")
+    valid = s[:, :, 4] > 0
+    span = (s[:, :, 4][valid].max() - s[:, :, 0][valid].min()) * TICK_NS / 1e3
+    print(f"persistent c4 step (28 layers x 4 linears, {G} workgroups): {span:.1f} us in the kernel, "
+          f"{span / (4 * sh.layers):.2f} us a phase")
+    print(f"{'linear':12s} {'wgs':>4s} {'start->wait':>11s} {'wait':>6s} {'QACT':>6s} {'rows':>6s} "
+          f"{'hand-off':>9s} {'tail':>6s}   (us; medians over workgroups, means over layers)")
+    for n, m in breakdown(s).items():
+        print(f"{n:12s} {m[6]:4.0f} {m[0]:11.2f} {m[1]:6.2f} {m[2]:6.2f} {m[3]:6.2f} {m[4]:9.2f} {m[5]:6.2f}")
+
+
+if __name__ == "__main__":
+    main()

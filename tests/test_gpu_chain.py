@@ -370,27 +370,30 @@ def test_chain_c4_layers_against_the_float64_emulation(X):
             assert err <= EMU_TOL * np.abs(me[k]).max(), (l, k, err / np.abs(me[k]).max())
 
 
-@pytest.mark.parametrize("fmt", ["fp4", "int4"])
-def test_chain_persistent_formats_and_shapes(X, fmt):
-    """The persistent step (otpu_chain_step) on fp4x6 and int4x weights at a shape whose phases
-    leave most workgroups without rows (hidden 512, q_dim 1024, F 1536, 4 layers, norms): the
-    oracle's step bit for bit, eager and over graph replays with new inputs, the error word 0."""
+@pytest.mark.parametrize("fmt,hidden,q_dim,kv_dim,F,layers", [("fp4", 512, 1024, 256, 1536, 4),
+                                                            ("int4", 512, 1024, 256, 1536, 4),
+                                                            ("int4", 1024, 2048, 512, 3840, 2)])
+def test_chain_persistent_formats_and_shapes(X, fmt, hidden, q_dim, kv_dim, F, layers):
+    """The persistent step (otpu_chain_step) on fp4x6 and int4x weights, at a shape whose phases
+    leave most workgroups without rows and at the largest F with 256-column down chunks (3840), with
+    per-layer norms: the oracle's step bit for bit, eager and over graph replays with new inputs,
+    the error word 0."""
     import torch
     from opentpu_amd.chain import DecodeChain, Shape
-    sh = Shape(hidden=512, q_dim=1024, kv_dim=256, F=1536, layers=4)
-    say("chain persistent", fmt)
+    sh = Shape(hidden=hidden, q_dim=q_dim, kv_dim=kv_dim, F=F, layers=layers)
+    say("chain persistent", fmt, hidden, q_dim, kv_dim, F, layers)
     base = DecodeChain.synthetic(sh, fmt, seed0=21, std=0.04)
     rng = np.random.default_rng(22)
-    norms = [(rng.uniform(0.5, 2.0, 512).astype(np.float32), rng.uniform(0.5, 2.0, 512).astype(np.float32))
+    norms = [(rng.uniform(0.5, 2.0, hidden).astype(np.float32), rng.uniform(0.5, 2.0, hidden).astype(np.float32))
              for _ in range(sh.layers)]
     ch = DecodeChain(base.layers, sh, fmt, True, norms)
-    assert ch.persistent
+    assert ch.persistent and ch.kernels_per_step == 1
     r = rng.uniform(0.5, 3.0, (sh.layers, 2)).astype(np.float32)
     ch.rnorm.copy_(torch.from_numpy(r).cuda())
     host = _host_layers(ch)
     onorms = [(norms[l][0], norms[l][1], r[l, 0:1], r[l, 1:2]) for l in range(sh.layers)]
-    xs = [rng.standard_normal((1, 512)).astype(np.float32) for _ in range(3)]
-    wants = [CH.step(x, host, fmt, 1024, 1536, onorms) for x in xs]
+    xs = [rng.standard_normal((1, hidden)).astype(np.float32) for _ in range(3)]
+    wants = [CH.step(x, host, fmt, q_dim, F, onorms) for x in xs]
     assert same_bits(ch.step(xs[0]).cpu().numpy(), wants[0])
     ch.capture()
     for i in range(4):
@@ -412,7 +415,7 @@ def test_chain_plan_refusals(X):
     arr = P4(p, p, p, p)
     for layers, hidden, q, kv, F, fmt in ((1, 2048, 2048, 512, 3072, 1), (1, 1024, 4096, 512, 3072, 1),
                                          (1, 1024, 2048, 512, 3200, 1), (1, 1024, 2048, 512, 3072, 0),
-                                         (1, 1024, 2048, 512, 6144, 2), (0, 1024, 2048, 512, 3072, 1)):
+                                         (1, 1024, 2048, 512, 4352, 2), (0, 1024, 2048, 512, 3072, 1)):
         with pytest.raises(OtpuError):
             X.call("otpu_chain_plan", layers, hidden, q, kv, F, fmt, arr, I4(512, 1024, 512, 1536), arr,
                    I4(64, 128, 64, 192), None, None, p, arr, p, 1 << 20)
