@@ -205,7 +205,7 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
                 return otpu_fail(OTPU_EINVAL, "chain_plan: layer %d phase %d row strides differ from layer 0's", l, k);
             if (l == 0) {
                 a.T = k == 0 ? QKV_T : k == 1 ? O_T : k == 2 ? GU_T : DN_T;
-                if (k == 3) a.ll_mul = F;
+                if (k == 2) a.gu_pair = F;                 // the fold reads g * u, F entries
                 hp.kind[k] = a;
             }
             ly[l].w[k] = w[j];

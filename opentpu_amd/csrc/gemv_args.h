@@ -39,13 +39,13 @@ struct MMArgs {
     // the persistent chain's hand-off rows (LL kernels only): 8-byte entries tag << 32 | fp32
     // bits, written with device-scope stores and polled with device-scope loads until every
     // entry a workgroup needs carries the phase's tag (no fences, no counters)
-    const uint64_t* ll_in;         // input entries (NULL: the plain row xin); xmul's at ll_in + ll_mul
+    const uint64_t* ll_in;         // input entries (NULL: the plain row xin)
     uint64_t* ll_out;              // output entries, besides the plain row out
-    int64_t ll_mul;
     uint32_t tag_in, tag_out;
     uint32_t* err;                 // set when a wait runs out of polls
     int spin;                      // polls a wait allows (~1 us each)
     int ll_all;                    // entries of the input row to wait for when more than K (see ll_drain)
+    int gu_pair;                   // F: gate/up rows taken in g / u pairs, the entries g * u (see gemv_body)
     uint64_t* stamp;               // the phase's clock stamps (builds with OTPU_PHASE_STAMPS only)
 };
 

@@ -60,8 +60,9 @@ struct FoldLds {
     float sa2s[FOLD_NRMAX];
 };
 
-// LL: a phase of the persistent chain: g and u from hand-off entries (a.ll_in, u at + a.ll_mul;
-// the weights and scale factors go out first), the output row also as entries, the caller's LDS
+// LL: a phase of the persistent chain: the input row mul(g, u) from hand-off entries (the gate/up
+// phase publishes the products; the weights and scale factors go out first), the output row
+// also as entries, the caller's LDS
 template <int FMT, int L, int T, bool LL = false>
 __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullptr) {
     static_assert(FMT != OTPU_INT8, "4-bit weights");
@@ -126,7 +127,7 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
         if (wave * NT < a.N) load(st, nfirst);
         __builtin_amdgcn_sched_barrier(0);
         OTPU_STAMP(a, 1);
-        ll_chunks<CPT, true>(a, NC, xv, gv);
+        ll_chunks<CPT>(a, NC, xv);
         OTPU_STAMP(a, 2);
     } else {
 #pragma unroll
@@ -154,7 +155,7 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
         float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
         if (c < NC) {
             t = xv[k];
-            if (LL || xm) {                              // VOP MUL
+            if (!LL && xm) {                             // VOP MUL
                 t.x = fmul(t.x, gv[k].x); t.y = fmul(t.y, gv[k].y); t.z = fmul(t.z, gv[k].z); t.w = fmul(t.w, gv[k].w);
             }
             if (a.rscale) { t.x = fmul(t.x, rf); t.y = fmul(t.y, rf); t.z = fmul(t.z, rf); t.w = fmul(t.w, rf); }

@@ -176,36 +176,30 @@ __device__ __forceinline__ void ll_store(uint64_t* p, uint32_t tag, float y) {
     __hip_atomic_store(p, ((uint64_t)tag << 32) | fbits(y), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// this thread's float4 chunks c = tid + 256 k (k < CPT, c < NC) of the entry row a.ll_in, and
-// with MUL of the row a.ll_in + a.ll_mul: every entry is loaded at once, then the entries that
-// do not carry a.tag_in yet are loaded again until they do.  A wait that runs out of polls sets
-// *a.err and goes on with what it has (the step's output is then invalid; every wave still ends).
-template <int CPT, bool MUL>
-__device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[CPT], float4 (&gv)[CPT]) {
-    constexpr int NR = MUL ? 2 : 1;
+// this thread's float4 chunks c = tid + 256 k (k < CPT, c < NC) of the entry row a.ll_in: every
+// entry is loaded at once, then the entries that do not carry a.tag_in yet are loaded again until
+// they do.  A wait that runs out of polls sets *a.err and goes on with what it has (the step's
+// output is then invalid; every wave still ends).
+template <int CPT>
+__device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[CPT]) {
     const int tid = threadIdx.x;
-    uint64_t e[NR][CPT][4];
+    uint64_t e[CPT][4];
 #pragma unroll
-    for (int h = 0; h < NR; ++h)
+    for (int k = 0; k < CPT; ++k) {
+        const int c = tid + 256 * k;
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) {
-            const int c = tid + 256 * k;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                e[h][k][j] = c < NC ? ll_load(a.ll_in + (h ? a.ll_mul : 0) + 4 * c + j) : (uint64_t)a.tag_in << 32;
-        }
+        for (int j = 0; j < 4; ++j) e[k][j] = c < NC ? ll_load(a.ll_in + 4 * c + j) : (uint64_t)a.tag_in << 32;
+    }
     for (int n = 0;; ++n) {
         bool done = true;
 #pragma unroll
-        for (int h = 0; h < NR; ++h)
+        for (int k = 0; k < CPT; ++k)
 #pragma unroll
-            for (int k = 0; k < CPT; ++k)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if ((uint32_t)(e[h][k][j] >> 32) != a.tag_in) {
-                        done = false;
-                        e[h][k][j] = ll_load(a.ll_in + (h ? a.ll_mul : 0) + 4 * (tid + 256 * k) + j);
-                    }
+            for (int j = 0; j < 4; ++j)
+                if ((uint32_t)(e[k][j] >> 32) != a.tag_in) {
+                    done = false;
+                    e[k][j] = ll_load(a.ll_in + 4 * (tid + 256 * k) + j);
+                }
         if (done) break;
         if (n >= a.spin) {
             __hip_atomic_fetch_or(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -214,13 +208,9 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
         if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
     }
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-        xv[k] = make_float4(bitsf((uint32_t)e[0][k][0]), bitsf((uint32_t)e[0][k][1]), bitsf((uint32_t)e[0][k][2]),
-                            bitsf((uint32_t)e[0][k][3]));
-        if (MUL)
-            gv[k] = make_float4(bitsf((uint32_t)e[NR - 1][k][0]), bitsf((uint32_t)e[NR - 1][k][1]),
-                                bitsf((uint32_t)e[NR - 1][k][2]), bitsf((uint32_t)e[NR - 1][k][3]));
-    }
+    for (int k = 0; k < CPT; ++k)
+        xv[k] = make_float4(bitsf((uint32_t)e[k][0]), bitsf((uint32_t)e[k][1]), bitsf((uint32_t)e[k][2]),
+                            bitsf((uint32_t)e[k][3]));
 }
 
 // wait for entries [from, to) of the input row as well, values unused: a phase that reads part of
@@ -330,7 +320,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
             issue_weights();
             __builtin_amdgcn_sched_barrier(0);
             OTPU_STAMP(a, 1);
-            ll_chunks<CPT, false>(a, NC, xv, gv);
+            ll_chunks<CPT>(a, NC, xv);
             if (a.ll_all > K) ll_drain(a, K, a.ll_all);
             OTPU_STAMP(a, 2);
         } else {
@@ -526,13 +516,21 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
     // offsets, so the loads take the saddr + voffset form; rows past N read the last row and
     // pieces past P the last piece (no branch around a load): the former reach no epilogue, the
     // latter meet zero activation registers
+    // LL gate/up pairs (gu_pair = F; 4 rows a team, 2 teams a wave): the 8 slots of the wave's
+    // group n0 are g rows n0/2 .. n0/2 + 3 and the u rows F after them, team t taking g and u of
+    // rows n0/2 + 2t, + 1 (slot r: u for r >= 2, row + (r & 1)), so each g sits 16 lanes below
+    // its u after the reduce-scatter
+    constexpr bool PAIRS = LL && R == 4 && NT == 2;
+    const int gp = PAIRS ? a.gu_pair : 0;
+    auto slot_row = [&](int r) { return (r >= 2 ? gp : 0) + 2 * team + (r & 1); };
     auto load = [&](Stage& st, int n0) {
-        const uint8_t* wb = w + (int64_t)n0 * a.rs;
-        const uint8_t* sb = ws + (int64_t)n0 * a.srs;
+        const int base = gp ? n0 / 2 : n0;
+        const uint8_t* wb = w + (int64_t)base * a.rs;
+        const uint8_t* sb = ws + (int64_t)base * a.srs;
         const int last = a.N - 1 - n0;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int dn = min(r * NT + team, last);
+            const int dn = gp ? slot_row(r) : min(r * NT + team, last);
             const uint32_t roff = (uint32_t)dn * (uint32_t)a.rs;
             const uint32_t soff = (uint32_t)dn * (uint32_t)a.srs;
 #pragma unroll
@@ -545,7 +543,8 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         }
         // (LL: flushed where it is used, so that issuing the loads waits for none of them and the
         // hand-off's polls go out at once)
-        const float swr = unit ? 1.0f : *reinterpret_cast<const float*>(sb + (uint32_t)min(er * NT + team, last) * (uint32_t)a.srs);
+        const int de = gp ? slot_row(er) : min(er * NT + team, last);
+        const float swr = unit ? 1.0f : *reinterpret_cast<const float*>(sb + (uint32_t)de * (uint32_t)a.srs);
         st.sw = LL ? swr : ftz(swr);
     };
     auto compute = [&](const Stage& st, int n0) {
@@ -576,6 +575,27 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         double tot = v[0];
 #pragma unroll
         for (; o > 0; o >>= 1) tot = xsum(tot, o);
+        if constexpr (LL) {                           // (QIN, one activation row, no flags)
+            // every lane forms its y (only the epilogue lanes' are kept): the pairs' exchange
+            // below needs the whole wave
+            const float y = fmul_f(fmul_f((float)tot, ftz(st.sw)), sa2[0]);
+            if (gp) {
+                const float yu = __uint_as_float(
+                    __builtin_amdgcn_permlane16_swap(fbits(y), fbits(y), false, false)[1]);
+                const int nl = n0 / 2 + slot_row(er);
+                if (epilane) {
+                    out[nl] = y;
+                    if (er < 2) ll_store(a.ll_out + nl, a.tag_out, fmul(y, yu));   // VOP MUL g * u
+                }
+            } else {
+                const int n = n0 + er * NT + team;
+                if (epilane && n < a.N) {
+                    out[n] = y;
+                    ll_store(a.ll_out + n, a.tag_out, y);
+                }
+            }
+            return;
+        }
         const int n = n0 + er * NT + team;
         if (epilane && n < a.N && ej < a.M) {
             if (a.acc_out) {
@@ -583,10 +603,9 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             } else {
                 // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw
                 // and the finished Sa * 2^-W need no operand flush
-                float y = fmul_f(fmul_f((float)tot, LL ? ftz(st.sw) : st.sw), sa2[ej]);
+                float y = fmul_f(fmul_f((float)tot, st.sw), sa2[ej]);
                 if constexpr (QIN) {                  // (no ACC / ASCALE / RMAX / LM head here)
                     out[(int64_t)ej * a.ors + n] = y;
-                    if constexpr (LL) ll_store(a.ll_out + n, a.tag_out, y);
                     return;
                 }
                 if (out) {
