@@ -11,10 +11,12 @@
 // device-scope loads (they bypass the XCDs' non-coherent L2s) until every entry carries the
 // phase's tag: no fences, no counters, no grid barrier (one with agent-scope release / acquire
 // costs ~30 us on MI355X, a hand-off ~2-3 us).  A phase issues its first weight rows before it
-// waits, so the weights stream in during the hand-off.  Two entry rows alternate: a workgroup
-// writes phase i + 2 into the row phase i used only after reading all of phase i + 1 (o waits
-// for k and v as well), which its producers wrote after they had read phase i; a workgroup
-// without rows in a phase reads nothing in it.
+// waits, so the weights stream in during the hand-off.  Three entry rows rotate: phase i + 3
+// writes the row phase i used.  Its writers have read all of phase i + 2, whose producers read
+// all of phase i + 1 (o reads only q, but every workgroup with q/k/v rows also has o rows, which
+// it writes after reading its q/k/v input; where a shape breaks that, o waits for k and v too),
+// whose producers wrote their entries after reading phase i.  A workgroup without rows in a
+// phase reads nothing in it.
 //
 // Tags.  Phase i of a call carries tag E * 4 L + i + 1, E the call's number: every workgroup
 // keeps its own call counter (read at the start, advanced at the end), so graph replays of the
@@ -71,15 +73,16 @@ struct ChainPlan {                               // device memory: the header, t
     const float* x0;                             // the step's input row
     const float* rnorm;                          // RSCALE factors [layers, 2] or NULL
     const ChainLayer* layer;
-    uint64_t* ll[2];                             // the alternating entry rows
+    uint64_t* ll[3];                             // the rotating entry rows
     uint32_t* calls;                             // call counter per workgroup
     uint32_t* err;
     int layers, fmt;
+    int kv_wait;                                 // o waits for the k and v entries as well
     uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
 };
 
 // rows of phase kind k the first iteration of workgroup b covers start at b * rows_per_wg(k)
-__device__ __forceinline__ int rows_per_wg(int k) {
+__host__ __device__ constexpr int rows_per_wg(int k) {
     return k == 0 ? 4 * (64 / QKV_T) * QKV_R : k == 1 ? 4 * (64 / O_T) * O_R : k == 2 ? 4 * (64 / GU_T) * GU_R : 4 * (64 / DN_T);
 }
 
@@ -108,14 +111,14 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             a.w = ly.w[k];
             a.ws = ly.ws[k];
             a.out = ly.out[k];
-            a.ll_in = i ? P.ll[(i - 1) & 1] : nullptr;
+            a.ll_in = i ? P.ll[(i - 1) % 3] : nullptr;
             a.xin = P.x0;
-            a.ll_out = P.ll[i & 1];
+            a.ll_out = P.ll[i % 3];
             a.tag_in = t0 + (uint32_t)i;
             a.tag_out = t0 + (uint32_t)i + 1;
             a.err = P.err;
             a.spin = CHAIN_SPIN;
-            a.ll_all = k == 1 ? P.kind[0].N : 0;         // o waits for k and v too
+            a.ll_all = k == 1 && P.kv_wait ? P.kind[0].N : 0;
             if (k == 0 || k == 2) {
                 a.rscale = P.rnorm ? P.rnorm + 2 * l + (k >> 1) : nullptr;
                 a.cscale = ly.cs[k >> 1];
@@ -148,7 +151,7 @@ static ChainLayout chain_layout(int layers, int maxn) {
     c.calls = c.layer + rnd256((int64_t)layers * sizeof(ChainLayer));
     c.ll = c.calls + rnd256((int64_t)(CHAIN_SLOTS + 1) * 4);       // the call counters, then the error word
     c.rowb = rnd256((int64_t)maxn * 8);
-    c.total = c.ll + 2 * c.rowb;
+    c.total = c.ll + 3 * c.rowb;
     return c;
 }
 
@@ -222,6 +225,14 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
     hp.err = hp.calls + CHAIN_SLOTS;
     hp.ll[0] = reinterpret_cast<uint64_t*>(base + lay.ll);
     hp.ll[1] = reinterpret_cast<uint64_t*>(base + lay.ll + lay.rowb);
+    hp.ll[2] = reinterpret_cast<uint64_t*>(base + lay.ll + 2 * lay.rowb);
+    // the rotation needs every workgroup with q/k/v rows to have o rows (see the top)
+    {
+        const int G = otpu_cu_count();
+        const int wq = std::min(G, (nq + rows_per_wg(0) - 1) / rows_per_wg(0));
+        const int wo = std::min(G, (hidden + rows_per_wg(1) - 1) / rows_per_wg(1));
+        hp.kv_wait = wq > wo;
+    }
     hp.layers = layers;
     hp.fmt = fmt;
     // synchronous copies: a plan is built once, outside any capture
