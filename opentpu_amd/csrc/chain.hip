@@ -27,6 +27,7 @@
 // (K <= 2048), the down projection 64 lanes with 2 pieces each (F <= 4096, F-chunks of 256).
 #include <algorithm>
 #include <cstddef>
+#include <cstdlib>
 #include <vector>
 
 #include "gemv_fold.h"
@@ -41,19 +42,19 @@ int fold_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const floa
               float* out);
 
 constexpr int CHAIN_SLOTS = 4096;               // workgroups' call counters a plan holds
-constexpr int CHAIN_SPIN = 1 << 16;             // polls a wait allows (~1 us each)
+constexpr int CHAIN_SPIN = 1 << 16;             // polls a wait allows (~1 us each; OTPU_CHAIN_SPIN at plan time)
 constexpr int CHAIN_PAD_LDS = 96 * 1024;        // dynamic LDS that keeps one workgroup a CU
 
 // the phases' teams: T lanes a row, R rows a team (the prologue QACT holds K <= 32 T elements)
 #ifndef OTPU_CHAIN_R
 #define OTPU_CHAIN_R 4
 #endif
-constexpr int QKV_T = 32, QKV_R = OTPU_CHAIN_R; // (the gate/up phase's body too: one copy of the code)
+constexpr int QKV_T = 32, QKV_R = OTPU_CHAIN_R; // (the gate/up phase's body too when R is 4: one copy)
 #ifndef OTPU_CHAIN_OR
 #define OTPU_CHAIN_OR 1
 #endif
 constexpr int O_T = 64, O_R = OTPU_CHAIN_OR;
-constexpr int GU_T = QKV_T, GU_R = QKV_R;
+constexpr int GU_T = 32, GU_R = 4;              // 4 rows a team, 2 teams a wave: the g / u pairs
 // the fold: 64 lanes a row (1024 rows on 256 workgroups; 32 lanes with 128 workgroups measured
 // 526 against 519 us a step)
 #ifndef OTPU_CHAIN_DNT
@@ -78,6 +79,7 @@ struct ChainPlan {                               // device memory: the header, t
     uint32_t* err;
     int layers, fmt;
     int kv_wait;                                 // o waits for the k and v entries as well
+    int spin;                                    // polls a wait allows
     uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
 };
 
@@ -91,7 +93,9 @@ union ChainLds {
     FoldLds f;
 };
 
-template <int FMT>
+// FIXED: the default poll limit as a constant (folded into the waits: a limit read from the plan
+// measured 16 us a step slower); the other copy serves plans with an OTPU_CHAIN_SPIN override
+template <int FMT, bool FIXED>
 __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     const int b = blockIdx.x;
     const uint32_t E = __hip_atomic_load(P.calls + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -117,7 +121,7 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             a.tag_in = t0 + (uint32_t)i;
             a.tag_out = t0 + (uint32_t)i + 1;
             a.err = P.err;
-            a.spin = CHAIN_SPIN;
+            a.spin = FIXED ? CHAIN_SPIN : P.spin;
             a.ll_all = k == 1 && P.kv_wait ? P.kind[0].N : 0;
             if (k == 0 || k == 2) {
                 a.rscale = P.rnorm ? P.rnorm + 2 * l + (k >> 1) : nullptr;
@@ -125,6 +129,7 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             }
             if (k == 1) gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
             else if (k == 3) fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
+            else if (k == 2 || QKV_R == GU_R) gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
             else gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
             OTPU_STAMP(a, 4);
             __syncthreads();                             // the next phase reuses the LDS
@@ -136,8 +141,14 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
 __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
     __shared__ __align__(16) ChainLds lds;
     const ChainPlan& P = *plan;
-    if (P.fmt == OTPU_INT4) chain_run<OTPU_INT4>(P, lds);
-    else chain_run<OTPU_FP4>(P, lds);
+    const bool fixed = P.spin == CHAIN_SPIN;
+    if (P.fmt == OTPU_INT4) {
+        if (fixed) chain_run<OTPU_INT4, true>(P, lds);
+        else chain_run<OTPU_INT4, false>(P, lds);
+    } else {
+        if (fixed) chain_run<OTPU_FP4, true>(P, lds);
+        else chain_run<OTPU_FP4, false>(P, lds);
+    }
 }
 
 static int64_t rnd256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -235,6 +246,13 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
     }
     hp.layers = layers;
     hp.fmt = fmt;
+    // the waits' poll limit: OTPU_CHAIN_SPIN (0 .. 2^20) overrides it, e.g. to drive the timeout
+    // path from the host in a test (every wait then gives up at once and sets the error word)
+    hp.spin = CHAIN_SPIN;
+    if (const char* e = getenv("OTPU_CHAIN_SPIN")) {
+        const long v = strtol(e, nullptr, 10);
+        if (v >= 0 && v <= (1 << 20)) hp.spin = (int)v;
+    }
     // synchronous copies: a plan is built once, outside any capture
     hipError_t e = hipMemset(base, 0, (size_t)lay.total);
     if (e == hipSuccess) e = hipMemcpy(base, &hp, sizeof(hp), hipMemcpyHostToDevice);

@@ -420,3 +420,27 @@ def test_chain_plan_refusals(X):
             X.call("otpu_chain_plan", layers, hidden, q, kv, F, fmt, arr, I4(512, 1024, 512, 1536), arr,
                    I4(64, 128, 64, 192), None, None, p, arr, p, 1 << 20)
     assert X.load().otpu_chain_plan_bytes(0, 1024, 2048, 512, 3072) == -1
+
+
+def test_chain_wait_timeout_sets_the_error_word(X, monkeypatch):
+    """The persistent step's bounded waits, driven from the host: with a poll limit of 0
+    (OTPU_CHAIN_SPIN, read when the plan is built) the waits give up at once, the step still
+    ends (every wave exits) and the plan's error word says the outputs are invalid; a plan with
+    the default limit on the same chain then runs clean and bit-exact."""
+    import torch
+    from opentpu_amd.chain import DecodeChain, Shape
+    sh = Shape(hidden=256, q_dim=512, kv_dim=256, F=768, layers=4)
+    base = DecodeChain.synthetic(sh, "int4", seed0=31, std=0.05)
+    x = np.random.default_rng(32).standard_normal((1, 256)).astype(np.float32)
+    want = CH.step(x, _host_layers(base), "int4", 512, 768)
+    monkeypatch.setenv("OTPU_CHAIN_SPIN", "0")
+    ch = DecodeChain(base.layers, sh, "int4")
+    say("chain timeout: spin 0")
+    for _ in range(3):
+        ch.step(x)
+    torch.cuda.synchronize()
+    assert ch.chain_error() == 1
+    monkeypatch.delenv("OTPU_CHAIN_SPIN")
+    ok = DecodeChain(base.layers, sh, "int4")
+    assert same_bits(ok.step(x).cpu().numpy(), want)
+    assert ok.chain_error() == 0
