@@ -94,8 +94,13 @@ union ChainLds {
 };
 
 // FIXED: the default poll limit as a constant (folded into the waits: a limit read from the plan
-// measured 16 us a step slower); the other copy serves plans with an OTPU_CHAIN_SPIN override
-template <int FMT, bool FIXED>
+// measured 16 us a step slower); the other copy serves plans with an OTPU_CHAIN_SPIN override.
+// C4: a copy for the Qwen3-0.6B shape (hidden 1024, q_dim 2048, kv_dim 1024, F 3072), its
+// phases' K, pieces and rows as constants
+#ifndef OTPU_CHAIN_C4
+#define OTPU_CHAIN_C4 1
+#endif
+template <int FMT, bool FIXED, bool C4>
 __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     const int b = blockIdx.x;
     const uint32_t E = __hip_atomic_load(P.calls + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -127,10 +132,18 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
                 a.rscale = P.rnorm ? P.rnorm + 2 * l + (k >> 1) : nullptr;
                 a.cscale = ly.cs[k >> 1];
             }
-            if (k == 1) gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
-            else if (k == 3) fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
-            else if (k == 2 || QKV_R == GU_R) gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
-            else gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
+            if (k == 1) {
+                if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; }
+                gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
+            } else if (k == 3) {
+                if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; }
+                fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
+            } else if (k == 2 || QKV_R == GU_R) {
+                if constexpr (C4) { a.K = 1024; a.P = 32; }
+                gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
+            } else {
+                gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
+            }
             OTPU_STAMP(a, 4);
             __syncthreads();                             // the next phase reuses the LDS
         }
@@ -142,12 +155,16 @@ __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
     __shared__ __align__(16) ChainLds lds;
     const ChainPlan& P = *plan;
     const bool fixed = P.spin == CHAIN_SPIN;
+    const bool c4 = OTPU_CHAIN_C4 && fixed && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 &&
+                    P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && !P.kv_wait;
     if (P.fmt == OTPU_INT4) {
-        if (fixed) chain_run<OTPU_INT4, true>(P, lds);
-        else chain_run<OTPU_INT4, false>(P, lds);
+        if (c4) chain_run<OTPU_INT4, true, true>(P, lds);
+        else if (fixed) chain_run<OTPU_INT4, true, false>(P, lds);
+        else chain_run<OTPU_INT4, false, false>(P, lds);
     } else {
-        if (fixed) chain_run<OTPU_FP4, true>(P, lds);
-        else chain_run<OTPU_FP4, false>(P, lds);
+        if (c4) chain_run<OTPU_FP4, true, true>(P, lds);
+        else if (fixed) chain_run<OTPU_FP4, true, false>(P, lds);
+        else chain_run<OTPU_FP4, false, false>(P, lds);
     }
 }
 
