@@ -100,6 +100,19 @@ union ChainLds {
 #ifndef OTPU_CHAIN_C4
 #define OTPU_CHAIN_C4 1
 #endif
+#ifndef OTPU_CHAIN_C4RS
+#define OTPU_CHAIN_C4RS 1
+#endif
+#ifndef OTPU_CHAIN_C4SPLIT
+#define OTPU_CHAIN_C4SPLIT 1
+#endif
+#define C4_RS(r, s)                 \
+    do {                            \
+        if (OTPU_CHAIN_C4RS) {      \
+            a.rs = (r);             \
+            a.srs = (s);            \
+        }                           \
+    } while (0)
 template <int FMT, bool FIXED, bool C4>
 __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     const int b = blockIdx.x;
@@ -132,14 +145,21 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
                 a.rscale = P.rnorm ? P.rnorm + 2 * l + (k >> 1) : nullptr;
                 a.cscale = ly.cs[k >> 1];
             }
+            // (C4: 4-bit rows of K / 2 bytes, scale rows of 8 + 8 ceil(K / 256) bytes)
             if (k == 1) {
-                if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; }
+                if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; C4_RS(1024, 72); }
                 gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
             } else if (k == 3) {
-                if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; }
+                if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; C4_RS(1536, 104); }
                 fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
+            } else if (C4 && OTPU_CHAIN_C4SPLIT && k == 0) {
+                if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 4096; a.gu_pair = 0; C4_RS(512, 40); }
+                gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
             } else if (k == 2 || QKV_R == GU_R) {
-                if constexpr (C4) { a.K = 1024; a.P = 32; }
+                if constexpr (C4) {
+                    a.K = 1024; a.P = 32; C4_RS(512, 40);
+                    if (OTPU_CHAIN_C4SPLIT) { a.N = 6144; a.gu_pair = 3072; }
+                }
                 gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
             } else {
                 gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
@@ -156,7 +176,9 @@ __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
     const ChainPlan& P = *plan;
     const bool fixed = P.spin == CHAIN_SPIN;
     const bool c4 = OTPU_CHAIN_C4 && fixed && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 &&
-                    P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && !P.kv_wait;
+                    P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && !P.kv_wait &&
+                    P.kind[0].rs == 512 && P.kind[0].srs == 40 && P.kind[1].rs == 1024 && P.kind[1].srs == 72 &&
+                    P.kind[2].rs == 512 && P.kind[2].srs == 40 && P.kind[3].rs == 1536 && P.kind[3].srs == 104;
     if (P.fmt == OTPU_INT4) {
         if (c4) chain_run<OTPU_INT4, true, true>(P, lds);
         else if (fixed) chain_run<OTPU_INT4, true, false>(P, lds);

@@ -372,10 +372,12 @@ def test_chain_c4_layers_against_the_float64_emulation(X):
 
 @pytest.mark.parametrize("fmt,hidden,q_dim,kv_dim,F,layers", [("fp4", 512, 1024, 256, 1536, 4),
                                                             ("int4", 512, 1024, 256, 1536, 4),
-                                                            ("int4", 1024, 2048, 512, 3840, 2)])
+                                                            ("int4", 1024, 2048, 512, 3840, 2),
+                                                            ("fp4", 1024, 2048, 1024, 3072, 2)])
 def test_chain_persistent_formats_and_shapes(X, fmt, hidden, q_dim, kv_dim, F, layers):
     """The persistent step (otpu_chain_step) on fp4x6 and int4x weights, at a shape whose phases
-    leave most workgroups without rows and at the largest F with 256-column down chunks (3840), with
+    leave most workgroups without rows, at the largest F with 256-column down chunks (3840) and at
+    the Qwen3-0.6B shape in fp4x6 (its shape-specialized copy; int4x is the c4 test's), with
     per-layer norms: the oracle's step bit for bit, eager and over graph replays with new inputs,
     the error word 0."""
     import torch
