@@ -69,6 +69,30 @@ def test_fake_act_ties_are_the_devices():
     assert np.array_equal(v[0], q[0].astype(np.float64))
 
 
+def test_fake_act_near_ties_defer_to_the_device():
+    """Near ties: float64's x / unit within 2^-31 of k + 1/2 without being one (an inexact
+    unit = amax / 127), found by a seeded search.  fake_act takes the device quantizer's value
+    there, and float64's own rint (a tie window of 0) disagrees with the device on a good share
+    of them: the window is what makes fake_act the device's at near ties."""
+    rng = np.random.default_rng(17)
+    amax = rng.uniform(1, 100, 20000).astype(np.float32)
+    s = amax.astype(np.float64) / 127
+    k = np.arange(4)
+    x = ((k[None, :] + 0.5) * s[:, None]).astype(np.float32)
+    r = x.astype(np.float64) / s[:, None]
+    dl = np.abs(r - (k[None, :] + 0.5))
+    i, j = np.nonzero((dl > 0) & (dl < 2.0 ** -31))
+    assert len(i) >= 100
+    i, j = i[:128], j[:128]
+    rows = np.zeros((len(i), 64), np.float32)
+    rows[:, 0] = amax[i]
+    rows[:, 1] = x[i, j]
+    v, _ = EM.fake_act(rows, row=True)
+    q = F.quantize_mx(rows, 32, row_mode=True)[0][:, 1].astype(np.float64)
+    assert np.array_equal(np.rint(v[:, 1] / s[i]), q)
+    assert (np.rint(r[i, j]) != q).sum() >= 16
+
+
 def test_mx_matmul_is_its_definition():
     rng = np.random.default_rng(3)
     M, N, K, W = 3, 5, 64, 6
