@@ -566,7 +566,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int
     tile_epilogue(a, sm.ring, sa2, m0, n0, acc, 16 - smax);
 }
 
+// C3: a copy for the c3 prefill shape (M 512, N 8192, K 2048, dense rows, RSC scale words), its
+// sizes and strides as constants (the kernel runs once a CU from a cold instruction cache)
+#ifndef OTPU_GEMM_C3
+#define OTPU_GEMM_C3 1
+#endif
+template <bool C3>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
+    if constexpr (C3) {
+        a.M = 512; a.N = 8192; a.K = 2048; a.ldq = 2048; a.rs = 2048; a.ldda = 64; a.srs = 4; a.ors = 8192;
+        a.tiles_m = 4; a.tiles_n = 64; a.vec4 = 1;
+    }
     __shared__ __align__(16) int8_t sRing[RING];
     __shared__ uint32_t sDa[2][GBM];       // the stage's four da bytes per activation row
     __shared__ uint8_t sDw[2][GBN];        // the stage's dw byte per weight row
@@ -723,6 +733,9 @@ int otpu_gemm_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* 
     a.tiles_m = (M + GBM - 1) / GBM;
     a.tiles_n = (N + GBN - 1) / GBN;
     a.vec4 = ((uintptr_t)out % 16 == 0) && (ors % 4 == 0);
-    gemm_i8_kernel<<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
+    const bool c3 = OTPU_GEMM_C3 && M == 512 && N == 8192 && K == 2048 && ldq == 2048 && rs == 2048 && ldda == 64 &&
+                    srs == 4 && ors == 8192 && a.vec4;
+    if (c3) gemm_i8_kernel<true><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
+    else gemm_i8_kernel<false><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
     return otpu_launch_check("mm gemm");
 }
