@@ -100,19 +100,7 @@ union ChainLds {
 #ifndef OTPU_CHAIN_C4
 #define OTPU_CHAIN_C4 1
 #endif
-#ifndef OTPU_CHAIN_C4RS
-#define OTPU_CHAIN_C4RS 1
-#endif
-#ifndef OTPU_CHAIN_C4SPLIT
-#define OTPU_CHAIN_C4SPLIT 1
-#endif
-#define C4_RS(r, s)                 \
-    do {                            \
-        if (OTPU_CHAIN_C4RS) {      \
-            a.rs = (r);             \
-            a.srs = (s);            \
-        }                           \
-    } while (0)
+
 template <int FMT, bool FIXED, bool C4>
 __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     const int b = blockIdx.x;
@@ -147,19 +135,16 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             }
             // (C4: 4-bit rows of K / 2 bytes, scale rows of 8 + 8 ceil(K / 256) bytes)
             if (k == 1) {
-                if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; C4_RS(1024, 72); }
+                if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; a.rs = 1024; a.srs = 72; }
                 gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
             } else if (k == 3) {
-                if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; C4_RS(1536, 104); }
+                if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; a.rs = 1536; a.srs = 104; }
                 fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
-            } else if (C4 && OTPU_CHAIN_C4SPLIT && k == 0) {
-                if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 4096; a.gu_pair = 0; C4_RS(512, 40); }
+            } else if (C4 && k == 0) {                   // (its own call site: its constants)
+                if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 4096; a.gu_pair = 0; a.rs = 512; a.srs = 40; }
                 gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
             } else if (k == 2 || QKV_R == GU_R) {
-                if constexpr (C4) {
-                    a.K = 1024; a.P = 32; C4_RS(512, 40);
-                    if (OTPU_CHAIN_C4SPLIT) { a.N = 6144; a.gu_pair = 3072; }
-                }
+                if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 6144; a.gu_pair = 3072; a.rs = 512; a.srs = 40; }
                 gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
             } else {
                 gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
@@ -309,11 +294,7 @@ extern "C" int otpu_chain_step(const void* plan, otpu_stream_t stream) {
                                    hipFuncAttributeMaxDynamicSharedMemorySize, CHAIN_PAD_LDS) == hipSuccess
                    ? CHAIN_PAD_LDS : 0;
     }();
-#ifndef OTPU_CHAIN_WGS
-#define OTPU_CHAIN_WGS 4096
-#endif
-    const int G = std::min(otpu_cu_count(), OTPU_CHAIN_WGS);
-    chain_kernel<<<(unsigned)G, 256, pad, (hipStream_t)stream>>>(static_cast<const ChainPlan*>(plan));
+    chain_kernel<<<(unsigned)otpu_cu_count(), 256, pad, (hipStream_t)stream>>>(static_cast<const ChainPlan*>(plan));
     return otpu_launch_check("chain_step");
 }
 
