@@ -121,6 +121,18 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             a.w = ly.w[k];
             a.ws = ly.ws[k];
             a.out = ly.out[k];
+            // what every chain phase shares, as constants (their branches drop out of the code):
+            // weights with scale rows from block 0, one input row, no VOP MUL, no batch
+            a.flags = 0;
+            a.k0 = 0;
+            a.M = 1;
+            a.nsum = 1;
+            a.xmul = nullptr;
+            a.acc_out = nullptr;
+            a.best = nullptr;
+            a.rmax_key = nullptr;
+            a.q_bs = a.sa_bs = a.da_bs = a.w_bs = a.ws_bs = a.out_bs = a.xin_bs = 0;
+            a.k0_bs = 0;
             a.ll_in = i ? P.ll[(i - 1) % 3] : nullptr;
             a.xin = P.x0;
             a.ll_out = P.ll[i % 3];
