@@ -79,6 +79,7 @@ struct ChainPlan {                               // device memory: the header, t
     uint32_t* err;
     int layers, fmt;
     int kv_wait;                                 // o waits for the k and v entries as well
+    int norms;                                   // RSCALE or CSCALE factors given
     int spin;                                    // polls a wait allows
     uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
 };
@@ -101,7 +102,8 @@ union ChainLds {
 #define OTPU_CHAIN_C4 1
 #endif
 
-template <int FMT, bool FIXED, bool C4>
+// NORMS: the plan has RSCALE / CSCALE factors (without them the factors are constant NULLs)
+template <int FMT, bool FIXED, bool C4, bool NORMS>
 __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     const int b = blockIdx.x;
     const uint32_t E = __hip_atomic_load(P.calls + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -141,7 +143,9 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             a.err = P.err;
             a.spin = FIXED ? CHAIN_SPIN : P.spin;
             a.ll_all = k == 1 && P.kv_wait ? P.kind[0].N : 0;
-            if (k == 0 || k == 2) {
+            a.rscale = nullptr;                          // (o and the fold have none)
+            a.cscale = nullptr;
+            if (NORMS && (k == 0 || k == 2)) {
                 a.rscale = P.rnorm ? P.rnorm + 2 * l + (k >> 1) : nullptr;
                 a.cscale = ly.cs[k >> 1];
             }
@@ -176,14 +180,17 @@ __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
                     P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && !P.kv_wait &&
                     P.kind[0].rs == 512 && P.kind[0].srs == 40 && P.kind[1].rs == 1024 && P.kind[1].srs == 72 &&
                     P.kind[2].rs == 512 && P.kind[2].srs == 40 && P.kind[3].rs == 1536 && P.kind[3].srs == 104;
+    const bool norms = P.norms != 0;
     if (P.fmt == OTPU_INT4) {
-        if (c4) chain_run<OTPU_INT4, true, true>(P, lds);
-        else if (fixed) chain_run<OTPU_INT4, true, false>(P, lds);
-        else chain_run<OTPU_INT4, false, false>(P, lds);
+        if (c4 && !norms) chain_run<OTPU_INT4, true, true, false>(P, lds);
+        else if (c4) chain_run<OTPU_INT4, true, true, true>(P, lds);
+        else if (fixed) chain_run<OTPU_INT4, true, false, true>(P, lds);
+        else chain_run<OTPU_INT4, false, false, true>(P, lds);
     } else {
-        if (c4) chain_run<OTPU_FP4, true, true>(P, lds);
-        else if (fixed) chain_run<OTPU_FP4, true, false>(P, lds);
-        else chain_run<OTPU_FP4, false, false>(P, lds);
+        if (c4 && !norms) chain_run<OTPU_FP4, true, true, false>(P, lds);
+        else if (c4) chain_run<OTPU_FP4, true, true, true>(P, lds);
+        else if (fixed) chain_run<OTPU_FP4, true, false, true>(P, lds);
+        else chain_run<OTPU_FP4, false, false, true>(P, lds);
     }
 }
 
@@ -282,6 +289,8 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
     }
     hp.layers = layers;
     hp.fmt = fmt;
+    hp.norms = rnorm != nullptr;
+    for (int j = 0; cscale && j < 2 * layers; ++j) hp.norms |= cscale[j] != nullptr;
     // the waits' poll limit: OTPU_CHAIN_SPIN (0 .. 2^20) overrides it, e.g. to drive the timeout
     // path from the host in a test (every wait then gives up at once and sets the error word)
     hp.spin = CHAIN_SPIN;
