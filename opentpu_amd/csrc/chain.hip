@@ -142,7 +142,7 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             a.tag_out = t0 + (uint32_t)i + 1;
             a.err = P.err;
             a.spin = FIXED ? CHAIN_SPIN : P.spin;
-            a.ll_all = k == 1 && P.kv_wait ? P.kind[0].N : 0;
+            a.ll_all = 0;
             a.rscale = nullptr;                          // (o and the fold have none)
             a.cscale = nullptr;
             if (NORMS && (k == 0 || k == 2)) {
@@ -151,6 +151,7 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             }
             // (C4: 4-bit rows of K / 2 bytes, scale rows of 8 + 8 ceil(K / 256) bytes)
             if (k == 1) {
+                if (P.kv_wait) a.ll_all = P.kind[0].N;       // o waits for k and v too
                 if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; a.rs = 1024; a.srs = 72; }
                 gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
             } else if (k == 3) {
@@ -158,10 +159,13 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
                 fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
             } else if (C4 && k == 0) {                   // (its own call site: its constants)
                 if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 4096; a.gu_pair = 0; a.rs = 512; a.srs = 40; }
-                gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
-            } else if (k == 2 || QKV_R == GU_R) {
+                if (i == 0) gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, false>(a, &lds.q);   // plain x0
+                else gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
+            } else if (k == 2) {
                 if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 6144; a.gu_pair = 3072; a.rs = 512; a.srs = 40; }
                 gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
+            } else if (i == 0) {                         // the step's first phase reads the plain x0
+                gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true, false>(a, &lds.q);
             } else {
                 gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
             }

@@ -262,10 +262,11 @@ struct QinLds {
 // waits for the row only, while the weights stream in (c4: 724 -> 659 us a step).  With a fold
 // (nsum > 1) the weights go first and the fold's loads after them (the other order measured
 // the same).
-// LL (the persistent chain): the row comes from hand-off entries when a.ll_in is set (the
-// weights and scale factors go out first: they do not wait for the hand-off), and the LDS is
-// the caller's (one block for all of the kernel's phases).
-template <int FMT, int L, int T, bool LL = false, typename IssueWeights>
+// LL (the persistent chain): the LDS is the caller's (one block for all of the kernel's
+// phases); LLIN: the row comes from the hand-off entries a.ll_in (the weights and scale factors
+// go out first: they do not wait for the hand-off), else from the plain row (the step's first
+// phase).
+template <int FMT, int L, int T, bool LL = false, bool LLIN = LL, typename IssueWeights>
 __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&act)[L][FMT == OTPU_INT8 ? 4 : 8],
                                              int (&shA)[L], float& sa2, IssueWeights&& issue_weights,
                                              QinLds* lds = nullptr) {
@@ -314,7 +315,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
     };
     if (a.nsum == 1) {
         float4 xv[CPT], gv[CPT];
-        if (LL && a.ll_in) {                             // (no VOP MUL in the chain's linears)
+        if (LLIN) {                                      // (no VOP MUL in the chain's linears)
             load_scales();
             __builtin_amdgcn_sched_barrier(0);
             issue_weights();
@@ -434,7 +435,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
 // the kernel body for a team of T lanes (T a compile-time constant: the exchanges of the
 // reduction are then straight-line code); QIN: the activation row is quantized in the prologue;
 // LL: a phase of the persistent chain (hand-off entries in and out, the caller's LDS)
-template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN, int R, bool LL = false>
+template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN, int R, bool LL = false, bool LLIN = LL>
 __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr) {
     constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
     constexpr int E = R * MR;                             // sums a lane carries per iteration
@@ -630,7 +631,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         // the first rows stream in while the workgroup quantizes the activation row
         Stage st;
         const int nfirst = wave * RW;
-        qin_prologue<FMT, L, T, LL>(a, b, act[0], shA[0], sa2[0], [&] {
+        qin_prologue<FMT, L, T, LL, LLIN>(a, b, act[0], shA[0], sa2[0], [&] {
             if (nfirst < a.N) load(st, nfirst);
         }, lds);
         if constexpr (LL) OTPU_STAMP(a, 3);
