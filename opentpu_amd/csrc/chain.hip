@@ -79,7 +79,7 @@ struct ChainPlan {                               // device memory: the header, t
     uint32_t* err;
     int layers, fmt;
     int kv_wait;                                 // o waits for the k and v entries as well
-    int norms;                                   // RSCALE or CSCALE factors given
+    int norms;                                   // 0 no RSCALE / CSCALE factors, 1 some, 2 both in every layer
     int spin;                                    // polls a wait allows
     uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
 };
@@ -102,9 +102,11 @@ union ChainLds {
 #define OTPU_CHAIN_C4 1
 #endif
 
-// NORMS: the plan has RSCALE / CSCALE factors (without them the factors are constant NULLs)
-template <int FMT, bool FIXED, bool C4, bool NORMS>
+// NORMS: 0 no RSCALE / CSCALE factors (constant NULLs), 1 some, 2 both in every layer (the
+// prologues' tests of the factors drop out)
+template <int FMT, bool FIXED, bool C4, int NORMS>
 __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
+    constexpr int NRM = NORMS == 0 ? 1 : NORMS == 2 ? 2 : 0;    // the prologues' factor flag
     const int b = blockIdx.x;
     const uint32_t E = __hip_atomic_load(P.calls + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int NL = P.layers;
@@ -145,7 +147,7 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             a.ll_all = 0;
             a.rscale = nullptr;                          // (o and the fold have none)
             a.cscale = nullptr;
-            if (NORMS && (k == 0 || k == 2)) {
+            if (NORMS != 0 && (k == 0 || k == 2)) {
                 a.rscale = P.rnorm ? P.rnorm + 2 * l + (k >> 1) : nullptr;
                 a.cscale = ly.cs[k >> 1];
             }
@@ -153,21 +155,21 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             if (k == 1) {
                 if (P.kv_wait) a.ll_all = P.kind[0].N;       // o waits for k and v too
                 if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; a.rs = 1024; a.srs = 72; }
-                gemv_body<FMT, 1, 1, O_T, false, true, O_R, true>(a, &lds.q);
+                gemv_body<FMT, 1, 1, O_T, false, true, O_R, true, true, 1>(a, &lds.q);
             } else if (k == 3) {
                 if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; a.rs = 1536; a.srs = 104; }
                 fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
             } else if (C4 && k == 0) {                   // (its own call site: its constants)
                 if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 4096; a.gu_pair = 0; a.rs = 512; a.srs = 40; }
-                if (i == 0) gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, false>(a, &lds.q);   // plain x0
-                else gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
+                if (i == 0) gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, false, NRM>(a, &lds.q);   // plain x0
+                else gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
             } else if (k == 2) {
                 if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 6144; a.gu_pair = 3072; a.rs = 512; a.srs = 40; }
-                gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true>(a, &lds.q);
+                gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
             } else if (i == 0) {                         // the step's first phase reads the plain x0
-                gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true, false>(a, &lds.q);
+                gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true, false, NRM>(a, &lds.q);
             } else {
-                gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true>(a, &lds.q);
+                gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true, true, NRM>(a, &lds.q);
             }
             OTPU_STAMP(a, 4);
             __syncthreads();                             // the next phase reuses the LDS
@@ -184,17 +186,18 @@ __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
                     P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && !P.kv_wait &&
                     P.kind[0].rs == 512 && P.kind[0].srs == 40 && P.kind[1].rs == 1024 && P.kind[1].srs == 72 &&
                     P.kind[2].rs == 512 && P.kind[2].srs == 40 && P.kind[3].rs == 1536 && P.kind[3].srs == 104;
-    const bool norms = P.norms != 0;
     if (P.fmt == OTPU_INT4) {
-        if (c4 && !norms) chain_run<OTPU_INT4, true, true, false>(P, lds);
-        else if (c4) chain_run<OTPU_INT4, true, true, true>(P, lds);
-        else if (fixed) chain_run<OTPU_INT4, true, false, true>(P, lds);
-        else chain_run<OTPU_INT4, false, false, true>(P, lds);
+        if (c4 && P.norms == 0) chain_run<OTPU_INT4, true, true, 0>(P, lds);
+        else if (c4 && P.norms == 2) chain_run<OTPU_INT4, true, true, 2>(P, lds);
+        else if (c4) chain_run<OTPU_INT4, true, true, 1>(P, lds);
+        else if (fixed) chain_run<OTPU_INT4, true, false, 1>(P, lds);
+        else chain_run<OTPU_INT4, false, false, 1>(P, lds);
     } else {
-        if (c4 && !norms) chain_run<OTPU_FP4, true, true, false>(P, lds);
-        else if (c4) chain_run<OTPU_FP4, true, true, true>(P, lds);
-        else if (fixed) chain_run<OTPU_FP4, true, false, true>(P, lds);
-        else chain_run<OTPU_FP4, false, false, true>(P, lds);
+        if (c4 && P.norms == 0) chain_run<OTPU_FP4, true, true, 0>(P, lds);
+        else if (c4 && P.norms == 2) chain_run<OTPU_FP4, true, true, 2>(P, lds);
+        else if (c4) chain_run<OTPU_FP4, true, true, 1>(P, lds);
+        else if (fixed) chain_run<OTPU_FP4, true, false, 1>(P, lds);
+        else chain_run<OTPU_FP4, false, false, 1>(P, lds);
     }
 }
 
@@ -293,8 +296,14 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
     }
     hp.layers = layers;
     hp.fmt = fmt;
-    hp.norms = rnorm != nullptr;
-    for (int j = 0; cscale && j < 2 * layers; ++j) hp.norms |= cscale[j] != nullptr;
+    {
+        bool any = rnorm != nullptr, all = rnorm != nullptr && cscale != nullptr;
+        for (int j = 0; cscale && j < 2 * layers; ++j) {
+            any = any || cscale[j] != nullptr;
+            all = all && cscale[j] != nullptr;
+        }
+        hp.norms = all ? 2 : any ? 1 : 0;
+    }
     // the waits' poll limit: OTPU_CHAIN_SPIN (0 .. 2^20) overrides it, e.g. to drive the timeout
     // path from the host in a test (every wait then gives up at once and sets the error word)
     hp.spin = CHAIN_SPIN;

@@ -266,7 +266,7 @@ struct QinLds {
 // phases); LLIN: the row comes from the hand-off entries a.ll_in (the weights and scale factors
 // go out first: they do not wait for the hand-off), else from the plain row (the step's first
 // phase).
-template <int FMT, int L, int T, bool LL = false, bool LLIN = LL, typename IssueWeights>
+template <int FMT, int L, int T, bool LL = false, bool LLIN = LL, int NRM = 0, typename IssueWeights>
 __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&act)[L][FMT == OTPU_INT8 ? 4 : 8],
                                              int (&shA)[L], float& sa2, IssueWeights&& issue_weights,
                                              QinLds* lds = nullptr) {
@@ -290,14 +290,17 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
     const int tid = threadIdx.x;
     const float* x = a.xin + b * a.xin_bs;
     const float* xm = a.xmul ? a.xmul + b * a.xin_bs : nullptr;
-    const float4* cs = a.cscale ? reinterpret_cast<const float4*>(a.cscale + b * a.xin_bs) : nullptr;
+    // NRM: 0 the RSCALE / CSCALE factors when given, 1 none, 2 both (known at compile time)
+    const bool has_r = NRM == 2 || (NRM == 0 && a.rscale != nullptr);
+    const bool has_c = NRM == 2 || (NRM == 0 && a.cscale != nullptr);
+    const float4* cs = has_c ? reinterpret_cast<const float4*>(a.cscale + b * a.xin_bs) : nullptr;
     float4 v[CPT], cv[CPT];
     float rf = 1.0f;
     uint32_t m = 0;
     // RSCALE / CSCALE factors, loaded with the row (QACT's pre-multiplies: (x * r) * c)
     auto load_scales = [&]() {
-        if (a.rscale) rf = *a.rscale;
-        if (cs) {
+        if (has_r) rf = *a.rscale;
+        if (has_c) {
 #pragma unroll
             for (int k = 0; k < CPT; ++k) {
                 const int c = tid + 256 * k;
@@ -306,8 +309,8 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
         }
     };
     auto finish = [&](float4 t, int k) {                 // VOP MUL done: pre-multiplies, flush, keep, row max
-        if (a.rscale) { t.x = fmul(t.x, rf); t.y = fmul(t.y, rf); t.z = fmul(t.z, rf); t.w = fmul(t.w, rf); }
-        if (cs) { t.x = fmul(t.x, cv[k].x); t.y = fmul(t.y, cv[k].y); t.z = fmul(t.z, cv[k].z); t.w = fmul(t.w, cv[k].w); }
+        if (has_r) { t.x = fmul(t.x, rf); t.y = fmul(t.y, rf); t.z = fmul(t.z, rf); t.w = fmul(t.w, rf); }
+        if (has_c) { t.x = fmul(t.x, cv[k].x); t.y = fmul(t.y, cv[k].y); t.z = fmul(t.z, cv[k].z); t.w = fmul(t.w, cv[k].w); }
         t.x = ftz(t.x); t.y = ftz(t.y); t.z = ftz(t.z); t.w = ftz(t.w);
         v[k] = t;
         m = max(m, max(max(fbits(t.x) & 0x7FFFFFFFu, fbits(t.y) & 0x7FFFFFFFu),
@@ -435,7 +438,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
 // the kernel body for a team of T lanes (T a compile-time constant: the exchanges of the
 // reduction are then straight-line code); QIN: the activation row is quantized in the prologue;
 // LL: a phase of the persistent chain (hand-off entries in and out, the caller's LDS)
-template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN, int R, bool LL = false, bool LLIN = LL>
+template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN, int R, bool LL = false, bool LLIN = LL, int NRM = 0>
 __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr) {
     constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
     constexpr int E = R * MR;                             // sums a lane carries per iteration
@@ -631,7 +634,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         // the first rows stream in while the workgroup quantizes the activation row
         Stage st;
         const int nfirst = wave * RW;
-        qin_prologue<FMT, L, T, LL, LLIN>(a, b, act[0], shA[0], sa2[0], [&] {
+        qin_prologue<FMT, L, T, LL, LLIN, NRM>(a, b, act[0], shA[0], sa2[0], [&] {
             if (nfirst < a.N) load(st, nfirst);
         }, lds);
         if constexpr (LL) OTPU_STAMP(a, 3);
