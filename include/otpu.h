@@ -194,8 +194,12 @@ int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float
  *   weights; hidden <= 1024, q_dim <= 2048, F a multiple of 256 and <= 4096, hidden and q_dim
  *   multiples of 32.
  *   otpu_chain_step: one step (reads x, writes every output row); capturable in a HIP graph.
+ *   Steps on one plan must not overlap (issue them on one stream).  A step needs all of its
+ *   workgroups (one a CU) resident at once: kernels beside it on other streams can hold CUs
+ *   back, and its waits then run out of polls (they are bounded: no hang).
  *   otpu_chain_error: the plan's error word (0: every hand-off completed; 1: a wait ran out of
- *   polls, the outputs since are invalid), synchronous. */
+ *   polls, the outputs since are invalid), synchronous.  It stays set until the plan is
+ *   written again. */
 int64_t otpu_chain_plan_bytes(int layers, int hidden, int q_dim, int kv_dim, int F);
 int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int fmt, const uint8_t* const* w,
                     const int64_t* rs, const uint8_t* const* ws, const int64_t* srs, const float* rnorm,

@@ -118,7 +118,8 @@ class DecodeChain:
         self.persistent = self.persistent_fits() if persistent is None else bool(persistent)
         if self.persistent and not self.persistent_fits():
             raise ValueError("DecodeChain: the persistent step needs fused, folded int4 / fp4 layers with "
-                             "hidden <= 1024, q_dim <= 2048, F <= 4096")
+                             "hidden <= 1024, q_dim <= 2048, F <= 4096 (and 2 kv_dim <= 2048 where o "
+                             "waits for k and v)")
 
     @staticmethod
     def synthetic(shape: Shape = Shape(), fmt: str = "int4", seed0: int = 100, std: float = 0.02,
@@ -218,8 +219,12 @@ class DecodeChain:
     def persistent_fits(self) -> bool:
         """Whether otpu_chain_step can run this chain (its phases' teams are compiled in)."""
         s = self.shape
+        # o waits for k and v as well when the q/k/v rows (32 a workgroup) span more workgroups
+        # than o's (4 a workgroup); that wait holds 2048 entries
+        kv_wait = -(-(s.q_dim + 2 * s.kv_dim) // 32) > -(-s.hidden // 4)
         return (self.fused and self.fold and self.fmt in ("int4", "fp4") and s.hidden <= 1024 and s.hidden % 32 == 0
-                and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 4096 and s.F % 256 == 0)
+                and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 4096 and s.F % 256 == 0
+                and not (kv_wait and 2 * s.kv_dim > 2048))
 
     def _use_persistent(self) -> bool:
         return self.persistent and self.fused and self.fold

@@ -293,6 +293,9 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
         const int wq = std::min(G, (nq + rows_per_wg(0) - 1) / rows_per_wg(0));
         const int wo = std::min(G, (hidden + rows_per_wg(1) - 1) / rows_per_wg(1));
         hp.kv_wait = wq > wo;
+        if (hp.kv_wait && 2 * kv_dim > 2048)             // (ll_drain's entries: 8 a thread)
+            return otpu_fail(OTPU_EINVAL, "chain_plan: o waits for k and v here, so 2 kv_dim must be <= 2048 (kv_dim %d)",
+                             kv_dim);
     }
     hp.layers = layers;
     hp.fmt = fmt;

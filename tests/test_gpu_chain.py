@@ -421,6 +421,11 @@ def test_chain_plan_refusals(X):
         with pytest.raises(OtpuError):
             X.call("otpu_chain_plan", layers, hidden, q, kv, F, fmt, arr, I4(512, 1024, 512, 1536), arr,
                    I4(64, 128, 64, 192), None, None, p, arr, p, 1 << 20)
+    # o waits for k and v when the q/k/v rows span more workgroups than o's (hidden 256: o on 64
+    # workgroups, q/k/v on 129); that wait holds 2048 entries
+    with pytest.raises(OtpuError, match="kv_dim"):
+        X.call("otpu_chain_plan", 1, 256, 2048, 1040, 768, 1, arr, I4(512, 1024, 512, 1536), arr,
+               I4(64, 128, 64, 192), None, None, p, arr, p, 1 << 20)
     assert X.load().otpu_chain_plan_bytes(0, 1024, 2048, 512, 3072) == -1
 
 
