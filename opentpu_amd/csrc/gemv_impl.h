@@ -683,17 +683,19 @@ __global__ __launch_bounds__(256) void gemv_qin_kernel(MMArgs a) {
     else gemv_body<FMT, 1, L, 16, PLAIN, true, R>(a);
 }
 
-// workgroups per CU the streaming grid aims for (measured on MI355X): 32 for one piece a lane
-// (the 80-problem c2: 6.61 TB/s against 6.36 at 16 and 6.48 at 64; each wave then streams one
-// or two row groups, so the last round of workgroups is short), 16 for four or more (the LM
-// head: the same from 16 to 64, 4% over 8), else 8; OTPU_GEMV_BLOCKS_PER_CU overrides
-inline int gemv_blocks_per_cu(int L) {
+// workgroups per CU the streaming grid aims for (measured on MI355X): for one piece a lane 32
+// with 4-bit weights (the 80-problem c2: 6.64 TB/s, steady over three runs, against 6.36 at
+// 16, 6.60-6.70 at 40-48 and 6.50-6.79 at 64; each wave streams one or two row groups, so the
+// last round of workgroups is short) and 64 with int8 (the 128-problem c1: 6.86-6.92 against
+// 6.59-6.62 TB/s at 32, one row group a wave); 16 for four or more pieces (the LM head: the
+// same from 16 to 64, 4% over 8), else 8; OTPU_GEMV_BLOCKS_PER_CU overrides
+inline int gemv_blocks_per_cu(int L, int fmt) {
     static const int v = [] {                   // read once (thread-safe static initialisation)
         const char* e = getenv("OTPU_GEMV_BLOCKS_PER_CU");
         const int x = e ? atoi(e) : 0;
         return (x > 0 && x <= 64) ? x : 0;
     }();
-    return v ? v : (L == 1 ? 32 : (L >= 4 ? 16 : 8));
+    return v ? v : (L == 1 ? (fmt == OTPU_INT8 ? 64 : 32) : (L >= 4 ? 16 : 8));
 }
 
 // rows a team takes per iteration (one activation row, one piece a lane) when the default
@@ -703,17 +705,17 @@ constexpr int R_SMALL = 4;
 // the grid of a launch with R rows a team: about gemv_blocks_per_cu workgroups per CU over the
 // whole batch, fewer when the rows run out (each wave then streams many row groups; its
 // activation registers are loaded once)
-inline int64_t gemv_blocks(const MMArgs& a, int R, int L, int batch) {
+inline int64_t gemv_blocks(const MMArgs& a, int fmt, int R, int L, int batch) {
     const int64_t waves = (a.N + (int64_t)R * (64 / a.T) - 1) / ((int64_t)R * (64 / a.T));
     int64_t blocks = (waves + 3) / 4;
-    int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L) / batch;
+    int64_t cap = (int64_t)otpu_cu_count() * gemv_blocks_per_cu(L, fmt) / batch;
     if (cap < 1) cap = 1;
     return blocks > cap ? cap : blocks;
 }
 
 template <int FMT, int MR, int L, int R>
 void launch_grid(const MMArgs& a, int batch, hipStream_t s) {
-    const int64_t blocks = gemv_blocks(a, R, L, batch);
+    const int64_t blocks = gemv_blocks(a, FMT, R, L, batch);
     if (a.flags & (OTPU_UNIT | OTPU_RSC))
         gemv_kernel<FMT, MR, L, true, R><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
     else
@@ -726,7 +728,7 @@ void launch_one(const MMArgs& a, int batch, hipStream_t s) {
     if constexpr (fits<FMT, MR, L>()) {
         constexpr int R = rows_per_team<L, MR>();
         if constexpr (MR == 1 && L == 1 && R > R_SMALL) {
-            if (gemv_blocks(a, R, L, batch) * batch < otpu_cu_count()) {
+            if (gemv_blocks(a, FMT, R, L, batch) * batch < otpu_cu_count()) {
                 launch_grid<FMT, MR, L, R_SMALL>(a, batch, s);
                 return;
             }
@@ -757,7 +759,7 @@ void launch_fmt(const MMArgs& a, int mr, int L, int batch, hipStream_t s) {
 
 template <int FMT, int L, int R>
 void launch_qin_grid(const MMArgs& a, int batch, hipStream_t s) {
-    const int64_t blocks = gemv_blocks(a, R, L, batch);
+    const int64_t blocks = gemv_blocks(a, FMT, R, L, batch);
     if (a.flags & (OTPU_UNIT | OTPU_RSC))
         gemv_qin_kernel<FMT, L, true, R><<<dim3((unsigned)blocks, batch), dim3(256), 0, s>>>(a);
     else
@@ -768,7 +770,7 @@ template <int FMT, int L>
 void launch_qin(const MMArgs& a, int batch, hipStream_t s) {
     constexpr int R = rows_per_team<L, 1>();
     if constexpr (L == 1 && R > R_SMALL) {
-        if (gemv_blocks(a, R, L, batch) * batch < otpu_cu_count()) {
+        if (gemv_blocks(a, FMT, R, L, batch) * batch < otpu_cu_count()) {
             launch_qin_grid<FMT, L, R_SMALL>(a, batch, s);
             return;
         }
