@@ -84,7 +84,9 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
     constexpr int NT = 64 / T;                    // teams a wave
     constexpr int GPT = T / FOLD_PPR;             // ranges a team slot holds
     const int K = a.K, NC = K >> 2, W = window_of(FMT), P = a.P, NR = K / FOLD_C;
-    const int tid = threadIdx.x, lane = tid & 63, tl = lane & (T - 1), team = lane / T;
+    // (workgroups of 256 threads: the mask tells the compiler so, and the chunk tests below then
+    // resolve at compile time where K is a constant)
+    const int tid = threadIdx.x & 255, lane = tid & 63, tl = lane & (T - 1), team = lane / T;
     const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + tid) >> 6);
     const int nwaves = (gridDim.x * blockDim.x) >> 6;
     const float* x = a.xin;
@@ -153,8 +155,8 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
     for (int k = 0; k < CPT; ++k) {
         const int c = tid + 256 * k;
         float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (LL || c < NC) t = xv[k];                     // (LL: entries past the row read as 0)
         if (c < NC) {
-            t = xv[k];
             if (!LL && xm) {                             // VOP MUL
                 t.x = fmul(t.x, gv[k].x); t.y = fmul(t.y, gv[k].y); t.z = fmul(t.z, gv[k].z); t.w = fmul(t.w, gv[k].w);
             }
@@ -162,38 +164,51 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
             if (cs) {                                    // RSCALE, then CSCALE: (x * r) * c
                 t.x = fmul(t.x, cv[k].x); t.y = fmul(t.y, cv[k].y); t.z = fmul(t.z, cv[k].z); t.w = fmul(t.w, cv[k].w);
             }
-            t.x = ftz(t.x); t.y = ftz(t.y); t.z = ftz(t.z); t.w = ftz(t.w);
+            // (hand-off entries are results of the FTZ arithmetic, flushed already, as are products)
+            if constexpr (!LL) { t.x = ftz(t.x); t.y = ftz(t.y); t.z = ftz(t.z); t.w = ftz(t.w); }
         }
         tv[k] = t;
         cm[k] = max(max(fbits(t.x) & 0x7FFFFFFFu, fbits(t.y) & 0x7FFFFFFFu),
                     max(fbits(t.z) & 0x7FFFFFFFu, fbits(t.w) & 0x7FFFFFFFu));
     }
 #pragma unroll
+    for (int k = 0; k < CPT; ++k)                          // the range's maximum, and on the way
+        am[k] = wave_max_dpp_64_8(cm[k], gm[k]);          // the 8 chunks' of this 32-group
+    // The chunks' quantization without branches (with one wave a SIMD a branch serializes what
+    // follows it; branch-free, the chunks' chains interleave): no test of the range maximum
+    // (recip(0) is 0, so a zero range quantizes to 0 and its Sa is 0) or of the group maximum
+    // (a zero group's offset selected as 0).  The LDS stores follow, under the chunk tests.
+    uint32_t qv[CPT];
+    int dgv[CPT];
+    float sav[CPT];
+#pragma unroll
     for (int k = 0; k < CPT; ++k) {
-        am[k] = wave_max_dpp(cm[k], 64);                  // the range's maximum
-        gm[k] = wave_max_dpp(cm[k], 8);                   // the 8 chunks of this 32-group
+        const uint32_t amax = am[k], g = gm[k];
+        const float fa = bitsf(amax);
+        // fmul(127, recip(fa)) and fmul(inv, 2^dg) as plain products: recip gives +0 or a normal
+        // number, so both are 0, normal or +inf (never a denormal or NaN to flush)
+        const float inv = 127.0f * recip(fa);
+        sav[k] = fmul(fmul(fa, bitsf(0x3C010204u)), pow2f(-W));
+        int dg = (int)(amax >> 23) - (int)(g >> 23) - ((g & 0x7FFFFFu) > (amax & 0x7FFFFFu));
+        dg = g ? (dg < 0 ? 0 : (dg > 31 ? 31 : dg)) : 0;
+        const float4 t = tv[k];
+        const float sc = inv * pow2f(dg);
+        // t and sc are flushed: q8 of the IEEE product is q8 of fmul's
+        qv[k] = (uint32_t)(q8(t.x * sc) & 0xFF) | ((uint32_t)(q8(t.y * sc) & 0xFF) << 8)
+              | ((uint32_t)(q8(t.z * sc) & 0xFF) << 16) | ((uint32_t)(q8(t.w * sc) & 0xFF) << 24);
+        dgv[k] = dg;
     }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
         const int c = tid + 256 * k;
         if (c >= NC) continue;                           // whole waves: uniform
-        const uint32_t amax = am[k];
-        const float fa = bitsf(amax);
-        const float inv = amax ? fmul(127.0f, recip(fa)) : 0.0f;
-        if (lane == 0) sa2s[c >> 6] = fmul(amax ? fmul(fa, bitsf(0x3C010204u)) : 0.0f, pow2f(-W));
-        int dg = 0;
-        if (gm[k]) {
-            dg = (int)(amax >> 23) - (int)(gm[k] >> 23) - ((gm[k] & 0x7FFFFFu) > (amax & 0x7FFFFFu));
-            dg = dg < 0 ? 0 : (dg > 31 ? 31 : dg);
-        }
-        const float4 t = tv[k];
-        const float sc = fmul(inv, pow2f(dg));
-        // t and sc are flushed: q8 of the IEEE product is q8 of fmul's
-        qs[c] = (uint32_t)(q8(t.x * sc) & 0xFF) | ((uint32_t)(q8(t.y * sc) & 0xFF) << 8)
-              | ((uint32_t)(q8(t.z * sc) & 0xFF) << 16) | ((uint32_t)(q8(t.w * sc) & 0xFF) << 24);
-        if ((c & 7) == 0) ds[c >> 3] = (uint8_t)dg;
+        if (lane == 0) sa2s[c >> 6] = sav[k];
+        qs[c] = qv[k];
+        if ((c & 7) == 0) ds[c >> 3] = (uint8_t)dgv[k];
     }
+    if constexpr (LL) OTPU_STAMP(a, 6);
     __syncthreads();
+    if constexpr (LL) OTPU_STAMP(a, 5);
 
     // 3. this lane's activation pieces (even / odd element bytes) and the ranges' Sa * 2^-W
     uint32_t act[L][8];

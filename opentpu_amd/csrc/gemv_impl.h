@@ -287,7 +287,9 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
     constexpr int CPT0 = (L * T * EPP / 4 + 255) / 256;
     constexpr int CPT = CPT0 < QIN_KMAX / 4 / 256 ? CPT0 : QIN_KMAX / 4 / 256;
     const int K = a.K, NC = K >> 2, W = window_of(FMT);
-    const int tid = threadIdx.x;
+    // (workgroups of 256 threads: the mask tells the compiler so, and the chunk tests below then
+    // resolve at compile time where K is a constant)
+    const int tid = threadIdx.x & 255;
     const float* x = a.xin + b * a.xin_bs;
     const float* xm = a.xmul ? a.xmul + b * a.xin_bs : nullptr;
     // NRM: 0 the RSCALE / CSCALE factors when given, 1 none, 2 both (known at compile time)
@@ -311,7 +313,8 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
     auto finish = [&](float4 t, int k) {                 // VOP MUL done: pre-multiplies, flush, keep, row max
         if (has_r) { t.x = fmul(t.x, rf); t.y = fmul(t.y, rf); t.z = fmul(t.z, rf); t.w = fmul(t.w, rf); }
         if (has_c) { t.x = fmul(t.x, cv[k].x); t.y = fmul(t.y, cv[k].y); t.z = fmul(t.z, cv[k].z); t.w = fmul(t.w, cv[k].w); }
-        t.x = ftz(t.x); t.y = ftz(t.y); t.z = ftz(t.z); t.w = ftz(t.w);
+        // (hand-off entries are results of the FTZ arithmetic, flushed already, as are products)
+        if constexpr (!LLIN) { t.x = ftz(t.x); t.y = ftz(t.y); t.z = ftz(t.z); t.w = ftz(t.w); }
         v[k] = t;
         m = max(m, max(max(fbits(t.x) & 0x7FFFFFFFu, fbits(t.y) & 0x7FFFFFFFu),
                        max(fbits(t.z) & 0x7FFFFFFFu, fbits(t.w) & 0x7FFFFFFFu)));
@@ -380,32 +383,51 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
         }
     }
     }
-    m = wave_max_dpp(m, 64);
+    // (one chunk a thread: m is that chunk's maximum, and the row maximum's wave reduction
+    // passes its 32-group's maximum on the way)
+    uint32_t g0 = 0;
+    if constexpr (CPT == 1) m = wave_max_dpp_64_8(m, g0);
+    else m = wave_max_dpp(m, 64);
     if ((tid & 63) == 0) red[tid >> 6] = m;
+    if constexpr (LL) OTPU_STAMP(a, 6);
     __syncthreads();
+    if constexpr (LL) OTPU_STAMP(a, 5);
     const uint32_t amax = max(max(red[0], red[1]), max(red[2], red[3]));
     const float fa = bitsf(amax);
-    const float inv = amax ? fmul(127.0f, recip(fa)) : 0.0f;
-    sa2 = fmul(amax ? fmul(fa, bitsf(0x3C010204u)) : 0.0f, pow2f(-W));
+    // no test of amax (recip(0) is 0: a zero row quantizes to 0 with Sa 0) or of a group's
+    // maximum (a zero group's offset selected as 0), and the LDS stores after the chunks'
+    // math: without branches the chunks' chains interleave (one wave a SIMD)
+    // fmul(127, recip(fa)) and fmul(inv, 2^dg) as plain products: recip gives +0 or a normal
+    // number, so both are 0, normal or +inf (never a denormal or NaN to flush)
+    const float inv = 127.0f * recip(fa);
+    sa2 = fmul(fmul(fa, bitsf(0x3C010204u)), pow2f(-W));
+    uint32_t qv[CPT];
+    int dgv[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        if (k * 256 >= NC) break;                        // uniform: the shuffles below converge
+        uint32_t gm = g0;
+        if constexpr (CPT > 1) {
+            gm = max(max(fbits(v[k].x) & 0x7FFFFFFFu, fbits(v[k].y) & 0x7FFFFFFFu),
+                     max(fbits(v[k].z) & 0x7FFFFFFFu, fbits(v[k].w) & 0x7FFFFFFFu));
+            gm = wave_max_dpp(gm, 8);                     // the 8 chunks of this 32-group
+        }
+        int dg = (int)(amax >> 23) - (int)(gm >> 23) - ((gm & 0x7FFFFFu) > (amax & 0x7FFFFFu));
+        dg = gm ? (dg < 0 ? 0 : (dg > 31 ? 31 : dg)) : 0;
+        const float sc = inv * pow2f(dg);
+        // v and sc are flushed: q8 of the IEEE product is q8 of fmul's (a denormal product
+        // rounds to 0 either way, NaN gives 0)
+        qv[k] = (uint32_t)(q8(v[k].x * sc) & 0xFF) | ((uint32_t)(q8(v[k].y * sc) & 0xFF) << 8)
+              | ((uint32_t)(q8(v[k].z * sc) & 0xFF) << 16) | ((uint32_t)(q8(v[k].w * sc) & 0xFF) << 24);
+        dgv[k] = dg;
+    }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
         const int c = tid + 256 * k;
-        if (k * 256 >= NC) break;                        // uniform: the shuffles below converge
-        uint32_t gm = max(max(fbits(v[k].x) & 0x7FFFFFFFu, fbits(v[k].y) & 0x7FFFFFFFu),
-                          max(fbits(v[k].z) & 0x7FFFFFFFu, fbits(v[k].w) & 0x7FFFFFFFu));
-        gm = wave_max_dpp(gm, 8);                         // the 8 chunks of this 32-group
-        int dg = 0;
-        if (gm) {
-            dg = (int)(amax >> 23) - (int)(gm >> 23) - ((gm & 0x7FFFFFu) > (amax & 0x7FFFFFu));
-            dg = dg < 0 ? 0 : (dg > 31 ? 31 : dg);
-        }
+        if (k * 256 >= NC) break;
         if (c < NC) {
-            const float sc = fmul(inv, pow2f(dg));
-            // v and sc are flushed: q8 of the IEEE product is q8 of fmul's (a denormal product
-            // rounds to 0 either way, NaN gives 0)
-            qs[c] = (uint32_t)(q8(v[k].x * sc) & 0xFF) | ((uint32_t)(q8(v[k].y * sc) & 0xFF) << 8)
-                  | ((uint32_t)(q8(v[k].z * sc) & 0xFF) << 16) | ((uint32_t)(q8(v[k].w * sc) & 0xFF) << 24);
-            if ((c & 7) == 0) ds[c >> 3] = (uint8_t)dg;
+            qs[c] = qv[k];
+            if ((c & 7) == 0) ds[c >> 3] = (uint8_t)dgv[k];
         }
     }
     __syncthreads();
