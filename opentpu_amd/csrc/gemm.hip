@@ -170,7 +170,8 @@ struct RingSrc {
 };
 
 __device__ __forceinline__ RingSrc ring_src(const GemmArgs& a, const int8_t* ring, int m0, int n0) {
-    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // (wave w mod 4: the loader waves 4-7 of gemm_lw_kernel issue what waves 0-3 would)
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & 3);
     RingSrc rs;
 #pragma unroll
     for (int u = 0; u < LPS / 2; ++u) {
@@ -566,10 +567,96 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int
     tile_epilogue(a, sm.ring, sa2, m0, n0, acc, 16 - smax);
 }
 
+// the barriers gemm_tile<true, MB> executes: K / 128 + 1 for each (d, e) pass it makes
+__device__ __forceinline__ int masked_barriers(int KT, uint32_t dmask, uint32_t emask, uint32_t smask, int smin,
+                                               int smax) {
+    int passes = 0;
+    for (int s = smin; s <= smax; ++s) {
+        if (!(smask >> s & 1)) continue;
+        for (int d = 0; d <= s; ++d) {
+            const int e = s - d;
+            if (!(dmask >> d & 1) || e > 16 || !(emask >> e & 1)) continue;
+            ++passes;
+        }
+    }
+    return passes * (KT + 1);
+}
+
+// ---- loader waves: workgroups of 8 waves, 4 of them streaming the ring, 4 multiplying ----
+// With one wave a SIMD doing both, a direct load that finds the load path full stalls the
+// wave's issue and the MFMAs behind it wait: a stage's loads and MFMAs add up instead of
+// overlapping.  Here waves 4-7 issue every direct load (the first NS - 1 stages before the
+// tile's offset scan) and waves 0-3 only read fragments and multiply; the two groups meet at
+// one barrier a stage.  A loader arrives once its part of stage kt has landed and then refills
+// the slot stage kt - 1 left; a compute wave arrives with its reads of stage kt - 1 done.
+// (c3 ROW x RSC: 18.5-18.7 -> 16.3-16.6 us back to back, bit-identical.)
+
+// a loader wave's walk (its first NS - 1 stages issued): KS + 1 barriers
+__device__ __forceinline__ void lw_load_walk(const RingSrc& rs, int KS) {
+    for (int kt = 0; kt < KS; ++kt) {
+        wait_stage(min(NS - 2, KS - 1 - kt));
+        ring_barrier();                                  // stage kt landed (this wave's part)
+        const int nk = kt + NS - 1;
+        if (nk < KS) ring_issue(rs, nk);
+    }
+    ring_barrier();
+}
+
+// a compute wave's walk: NP planes into acc[p]; MASK: each stage's A fragments masked to plane
+// p's 32-groups (plain weights, offsets from da_lds as in gemm_pass_mp), else the single plane.
+// KS + 1 barriers, matching lw_load_walk's.
+template <int NP, bool MASK>
+__device__ __forceinline__ void lw_mma_walk(const int8_t* ring, const uint32_t* da_lds, v4i (&acc)[NP][4][4],
+                                            const int (&dv)[MP_MAX], int KS) {
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wid >> 1, wn = wid & 1;
+    for (int kt = 0; kt < KS; ++kt) {
+        ring_barrier();                                  // stage kt landed everywhere
+        const int8_t* A = ring + (kt % NS) * STAGE;
+        const int8_t* B = A + TILE;
+        uint32_t dw4[4] = {0u, 0u, 0u, 0u};
+        if constexpr (MASK) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dw4[i] = da_lds[(wm * 64 + i * 16 + (lane & 15)) * DAS + kt];
+        }
+        v4i fa[2][4], fb[2][4];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int c = ks * 4 + (lane >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fa[ks][i] = *reinterpret_cast<const v4i*>(A + rof(wm * 64 + i * 16 + (lane & 15), c));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fb[ks][j] = *reinterpret_cast<const v4i*>(B + rof(wn * 64 + j * 16 + (lane & 15), c));
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int gsh = 8 * ((ks * 4 + (lane >> 4)) >> 1);   // the chunk's 32-group offset byte
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                v4i fm[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool keep = !MASK || ((dw4[i] >> gsh) & 0xFFu) == (uint32_t)dv[p];
+                    fm[i] = keep ? fa[ks][i] : v4i{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[p][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fm[i], fb[ks][j], acc[p][i][j], 0, 0, 0);
+            }
+        }
+    }
+    ring_barrier();                                      // every read of the ring done
+}
+
 // C3: a copy for the c3 prefill shape (M 512, N 8192, K 2048, dense rows, RSC scale words), its
 // sizes and strides as constants (the kernel runs once a CU from a cold instruction cache)
 #ifndef OTPU_GEMM_C3
 #define OTPU_GEMM_C3 1
+#endif
+#ifndef OTPU_GEMM_LW
+#define OTPU_GEMM_LW 1                  // the C3 shape with loader waves (gemm_lw_kernel)
 #endif
 template <bool C3>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
@@ -715,6 +802,183 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     else gemm_tile<true, true>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sSa2);
 }
 
+// The C3 shape with loader waves (workgroups of 8 waves).  Waves 0-3 run everything
+// gemm_i8_kernel's waves run (the offset scan, the epilogue, the masked passes); waves 4-7
+// issue the ring's direct loads.  Tiles of one plane, or of one or two activation planes with
+// plain weights, walk the ring with both groups; every other tile waits for the loaders' stages
+// to land and runs on waves 0-3 alone, the loaders matching its barriers one for one
+// (the masked passes') or leaving when none follow.
+template <bool C3>
+__global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
+    if constexpr (C3) {
+        a.M = 512; a.N = 8192; a.K = 2048; a.ldq = 2048; a.rs = 2048; a.ldda = 64; a.srs = 4; a.ors = 8192;
+        a.tiles_m = 4; a.tiles_n = 64; a.vec4 = 1;
+    }
+    __shared__ __align__(16) int8_t sRing[RING];
+    __shared__ uint32_t sDa[2][GBM];
+    __shared__ uint8_t sDw[2][GBN];
+    __shared__ uint32_t sMask[8];
+    __shared__ uint32_t sDaAll[GBM * DAS];
+    __shared__ float sSa2[GBM];
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool loader = wid >= 4;
+    int b = blockIdx.x, tm, tn;
+    const int ntiles = a.tiles_m * a.tiles_n;
+    if (ntiles % 8 == 0 && a.tiles_n % 8 == 0) {
+        const int per = ntiles / 8, x = b % 8, li = b / 8;
+        const int t = x * per + li;
+        tn = t / a.tiles_m;
+        tm = t % a.tiles_m;
+    } else {
+        tn = b / a.tiles_m;
+        tm = b % a.tiles_m;
+    }
+    const int m0 = tm * GBM, n0 = tn * GBN;
+    const bool unit = (a.flags & OTPU_UNIT) != 0;
+    const bool plain = unit || (a.flags & OTPU_RSC) != 0;
+    const int KT = a.K / GBK, KS = a.K / RBK;
+
+    const RingSrc rs = ring_src(a, sRing, m0, n0);
+    if (loader) {
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s)
+            if (s < KS) ring_issue(rs, s);
+    } else {
+        if (tid < GBM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-16)) : 0.0f;
+        // the offsets present in this tile, as gemm_i8_kernel finds them (waves 0-3)
+        uint32_t dm = 0, em = 0;
+        const int r = tid & (GBM - 1), h = tid >> 7;
+        if (m0 + r < a.M) {
+            const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)(m0 + r) * a.ldda);
+#pragma unroll 8
+            for (int k = h; k < KT; k += 2) {
+                const uint32_t wd = drow[k];
+                if (KT <= MP_KT) sDaAll[r * DAS + k] = wd;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t d = (wd >> (8 * t)) & 0xFF;
+                    dm |= 1u << (d <= 16 ? d : 17);
+                }
+            }
+        }
+        if (plain) {
+            em = 1u;
+        } else if (n0 + r < a.N) {
+            const uint8_t* wrow = a.ws + (int64_t)(n0 + r) * a.srs + 4 + a.k0;
+#pragma unroll 8
+            for (int k = h; k < KT; k += 2) {
+                const uint32_t e = wrow[k];
+                em |= 1u << (e <= 16 ? e : 17);
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            dm |= __shfl_xor(dm, o, 64);
+            em |= __shfl_xor(em, o, 64);
+        }
+        if (lane == 0) {
+            sMask[2 * wid] = dm;
+            sMask[2 * wid + 1] = em;
+        }
+    }
+    __syncthreads();
+    uint32_t dall = 0, eall = 0;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+        dall |= sMask[2 * x];
+        eall |= sMask[2 * x + 1];
+    }
+    const uint32_t dmask = dall & 0x1FFFFu, emask = eall & 0x1FFFFu;
+    const bool over = ((dall | eall) >> 17) & 1;
+    uint32_t smask = 0;
+    for (int d = 0; d <= 16; ++d)
+        if (dmask >> d & 1) smask |= (emask << d) & 0x1FFFFu;
+    const int smin = smask ? __builtin_ctz(smask) : 0, smax = smask ? 31 - __builtin_clz(smask) : 0;
+    const bool fits = smask && (int64_t)a.K * 16129 <= (((int64_t)1 << 31) - 1) >> (smax - smin);
+    const bool single = !over && __builtin_popcount(dmask) == 1 && __builtin_popcount(emask) == 1;
+    const int np = __builtin_popcount(dmask);
+    const bool mp = !single && plain && KT <= MP_KT && np >= 1 && np <= 2;
+
+    if (fits && (single || mp)) {
+        if (loader) {
+            lw_load_walk(rs, KS);
+            return;
+        }
+        int dv[MP_MAX];
+        uint32_t left = dmask;
+#pragma unroll
+        for (int p = 0; p < MP_MAX; ++p) {               // the planes' d in ascending order
+            dv[p] = left ? __builtin_ctz(left) : 255;
+            left &= left - 1;
+        }
+        if (single || np == 1) {                         // (one plane of plain weights: no masking
+            v4i acc[1][4][4];                            // when its offset covers every group)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[0][i][j] = v4i{0, 0, 0, 0};
+            if (single) lw_mma_walk<1, false>(sRing, sDaAll, acc, dv, KS);
+            else lw_mma_walk<1, true>(sRing, sDaAll, acc, dv, KS);
+            tile_epilogue(a, sRing, sSa2, m0, n0, acc[0], 16 - smax);
+        } else {
+            v4i acc[2][4][4];
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[p][i][j] = v4i{0, 0, 0, 0};
+            lw_mma_walk<2, true>(sRing, sDaAll, acc, dv, KS);
+            // sum_p C_p << (smax - d_p) (the bound checked above)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[0][i][j] = (acc[0][i][j] << (smax - dv[0])) + (acc[1][i][j] << (smax - dv[1]));
+            tile_epilogue(a, sRing, sSa2, m0, n0, acc[0], 16 - smax);
+        }
+        return;
+    }
+    // every other tile: the loaders' stages land, then waves 0-3 alone
+    if (loader) {
+        wait_dma<0>();
+        ring_barrier();
+        const int nb = (smask && fits) ? masked_barriers(KT, dmask, emask, smask, smin, smax) : 0;
+        for (int i = 0; i < nb; ++i) __syncthreads();    // the masked passes' barriers
+        return;
+    }
+    ring_barrier();
+    if (smask == 0) {                                    // every group drops: acc = 0
+        v4i z[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) z[i][j] = v4i{0, 0, 0, 0};
+        tile_epilogue(a, sRing, sSa2, m0, n0, z, 0);
+        return;
+    }
+    if (!fits) {
+        for (int idx = tid; idx < GBM * GBN; idx += 256) {
+            const int r = idx / GBN, c = idx % GBN;
+            const int m = m0 + r, n = n0 + c;
+            if (m < a.M && n < a.N) {
+                float y = fmul(fmul(i2f(valu_acc(a, m, n, plain)),
+                                    unit ? 1.0f : *reinterpret_cast<const float*>(a.ws + (int64_t)n * a.srs)),
+                               fmul(a.Sa[m], pow2f(-16)));
+                float* o = a.out + (int64_t)m * a.ors + n;
+                if (a.flags & OTPU_ASCALE) y = fadd(fmul(*o, a.alpha[m]), y);
+                else if (a.flags & OTPU_ACC) y = fadd(*o, y);
+                *o = y;
+            }
+        }
+        return;
+    }
+    const Smem sm{reinterpret_cast<int8_t(*)[GBM * GBK]>(sRing),
+                  reinterpret_cast<int8_t(*)[GBN * GBK]>(sRing + 2 * GBM * GBK), sDa, sDw, sRing};
+    if (plain) gemm_tile<true, false>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sSa2);
+    else gemm_tile<true, true>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sSa2);
+}
+
 }  // namespace otpu
 
 using namespace otpu;
@@ -735,7 +999,8 @@ int otpu_gemm_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* 
     a.vec4 = ((uintptr_t)out % 16 == 0) && (ors % 4 == 0);
     const bool c3 = OTPU_GEMM_C3 && M == 512 && N == 8192 && K == 2048 && ldq == 2048 && rs == 2048 && ldda == 64 &&
                     srs == 4 && ors == 8192 && a.vec4;
-    if (c3) gemm_i8_kernel<true><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
+    if (c3 && OTPU_GEMM_LW) gemm_lw_kernel<true><<<a.tiles_m * a.tiles_n, 512, 0, s>>>(a);
+    else if (c3) gemm_i8_kernel<true><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
     else gemm_i8_kernel<false><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
     return otpu_launch_check("mm gemm");
 }

@@ -459,6 +459,31 @@ def test_gemm_acc_ascale(ops):
                                 old=old, alpha=alpha))
 
 
+def test_gemm_c3_shape_tile_kinds(ops):
+    """The c3 shape's kernel (loader waves beside the MFMA waves) on every kind of tile: each
+    128-row tile's activation offsets drawn from its own set -- three planes (the masked passes,
+    the loader waves matching their barriers), offsets 9 apart (the exact VALU path), all past
+    the window (a zero tile), two planes without offset 0 (the two-plane walk) -- every output
+    bit against the C oracle."""
+    import torch
+    _, quant, mxu = ops
+    M, K, N = 512, 2048, 8192
+    rng = np.random.default_rng(17)
+    q = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    Sa = (np.abs(rng.standard_normal(M)) + 0.5).astype(np.float32)
+    da = np.zeros((M, K // 32), np.uint8)
+    for t, dset in enumerate([(0, 1, 2), (0, 9), (20,), (1, 3)]):
+        da[128 * t:128 * (t + 1)] = np.asarray(dset, np.uint8)[rng.integers(0, len(dset), (128, K // 32))]
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    rows_d, srows_d = quant.quantize_mxu(torch.randn((N, K), generator=gen, device="cuda") * 0.02, "int8", rsc=True)
+    rows, srows = rows_d.cpu().numpy(), srows_d.cpu().numpy()
+    say("gemm c3 shape: tile kinds")
+    got = mxu.mm(q, Sa, da, rows, srows, "int8", K, rsc=True)
+    want = OC.mm(q, Sa, da, rows, srows, "int8", K, flags=MM.RSC)
+    assert same_bits(got, want)
+    assert not np.any(got[256:384]), "offsets past the window: the tile drops every group"
+
+
 def test_gemm_c3_full_size(ops):
     """c3: M=512 x K=2048 x N=8192, ROW activations x RSC weights (the headline GEMM) and MX
     activations (the plane path), every output bit against the C oracle."""
