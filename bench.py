@@ -401,7 +401,7 @@ def main():
         extra["c4_decode_step_launches"] = c4_step(10, 2, persistent=False)
         print(f"[c4 launches] {extra['c4_decode_step_launches']}", file=sys.stderr, flush=True)
     if "c3" in only or "c3r" in only:
-        ms3 = gemm(5, 1)
+        ms3 = gemm(20, 2)
         tops = 2 * 512 * 2048 * 8192 / (ms3 * 1e-3) / 1e12
         extra["c3_gemm_row_x_rsc"] = {"us": round(ms3 * 1e3, 2), "TOPS": round(tops, 2),
                                       "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
@@ -412,7 +412,7 @@ def main():
         del o3
         extra["c3_output_write_alone"] = {"us": round(msf * 1e3, 2), "what": "torch fill_ of the 512 x 8192 fp32 output"}
     if "c3" in only or "c3m" in only:
-        ms3m = gemm(5, 1, row_mode=False)
+        ms3m = gemm(20, 2, row_mode=False)
         tops = 2 * 512 * 2048 * 8192 / (ms3m * 1e-3) / 1e12
         extra["c3_gemm_mx_x_rsc"] = {"us": round(ms3m * 1e3, 2), "TOPS": round(tops, 2),
                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
