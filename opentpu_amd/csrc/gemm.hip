@@ -656,7 +656,7 @@ __device__ __forceinline__ void lw_mma_walk(const int8_t* ring, const uint32_t* 
 #define OTPU_GEMM_C3 1
 #endif
 #ifndef OTPU_GEMM_LW
-#define OTPU_GEMM_LW 1                  // the C3 shape with loader waves (gemm_lw_kernel)
+#define OTPU_GEMM_LW 1                  // loader waves (gemm_lw_kernel); 0: gemm_i8_kernel's one wave group
 #endif
 template <bool C3>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
@@ -802,7 +802,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
     else gemm_tile<true, true>(a, sm, m0, n0, dmask, emask, smask, smin, smax, sSa2);
 }
 
-// The C3 shape with loader waves (workgroups of 8 waves).  Waves 0-3 run everything
+// The GEMM with loader waves (workgroups of 8 waves; C3: the c3 shape's copy).  Waves 0-3 run everything
 // gemm_i8_kernel's waves run (the offset scan, the epilogue, the masked passes); waves 4-7
 // issue the ring's direct loads.  Tiles of one plane, or of one or two activation planes with
 // plain weights, walk the ring with both groups; every other tile waits for the loaders' stages
@@ -999,8 +999,12 @@ int otpu_gemm_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* 
     a.vec4 = ((uintptr_t)out % 16 == 0) && (ors % 4 == 0);
     const bool c3 = OTPU_GEMM_C3 && M == 512 && N == 8192 && K == 2048 && ldq == 2048 && rs == 2048 && ldda == 64 &&
                     srs == 4 && ors == 8192 && a.vec4;
-    if (c3 && OTPU_GEMM_LW) gemm_lw_kernel<true><<<a.tiles_m * a.tiles_n, 512, 0, s>>>(a);
-    else if (c3) gemm_i8_kernel<true><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
-    else gemm_i8_kernel<false><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
+    if (OTPU_GEMM_LW) {
+        if (c3) gemm_lw_kernel<true><<<a.tiles_m * a.tiles_n, 512, 0, s>>>(a);
+        else gemm_lw_kernel<false><<<a.tiles_m * a.tiles_n, 512, 0, s>>>(a);
+    } else {
+        if (c3) gemm_i8_kernel<true><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
+        else gemm_i8_kernel<false><<<a.tiles_m * a.tiles_n, 256, 0, s>>>(a);
+    }
     return otpu_launch_check("mm gemm");
 }
