@@ -433,6 +433,59 @@ __device__ __forceinline__ void gemm_pass_mp(const GemmArgs& a, int8_t* ring, co
 // (every wave is past its last read of the ring when the epilogue starts).
 constexpr int TPS = 68;                         // transpose row stride, words
 
+// a wave's 64 x 64 accumulators into its transpose region T (rows TPS words apart)
+__device__ __forceinline__ void epi_transpose(int* T, const v4i (&acc)[4][4]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) T[(16 * i + 4 * (lane >> 4) + t) * TPS + 16 * j + (lane & 15)] = acc[i][j][t];
+}
+
+// row groups s0 .. s1 - 1 of region w's 16 (region w: the 64 x 64 of wave w) from T, scaled and
+// stored as 4-row x 256-byte float4 rows
+__device__ __forceinline__ void epi_rows(const GemmArgs& a, const int* T, const float* sa2, int m0, int n0, int w,
+                                         int s0, int s1, int sh) {
+    const int lane = threadIdx.x & 63;
+    const bool unit = (a.flags & OTPU_UNIT) != 0;
+    const int q = lane & 15, g = lane >> 4;
+    const int rt = (w >> 1) * 64 + g;                          // the tile row of group s = 0
+    const int nc = n0 + (w & 1) * 64 + 4 * q;
+    float sw[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sw[c] = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(a.ws + (int64_t)(nc + c) * a.srs));
+    const bool asc = (a.flags & OTPU_ASCALE) != 0, accf = (a.flags & OTPU_ACC) != 0;
+#pragma unroll 2
+    for (int s = s0; s < s1; ++s) {
+        const int r = rt + 4 * s;
+        const int4 raw = *reinterpret_cast<const int4*>(T + (g + 4 * s) * TPS + 4 * q);
+        const float sa = sa2[r];
+        float y[4] = {ldexpf((float)raw.x, sh), ldexpf((float)raw.y, sh), ldexpf((float)raw.z, sh),
+                      ldexpf((float)raw.w, sh)};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = fmul_f(fmul_f(y[c], sw[c]), sa);
+        float* p = a.out + (int64_t)(m0 + r) * a.ors + nc;
+        if (asc || accf) {
+            const float4 old = *reinterpret_cast<const float4*>(p);
+            const float o[4] = {old.x, old.y, old.z, old.w};
+            const float al = asc ? a.alpha[m0 + r] : 1.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) y[c] = asc ? fadd(fmul(o[c], al), y[c]) : fadd(o[c], y[c]);
+        }
+#ifndef OTPU_GEMM_NT_STORE
+#define OTPU_GEMM_NT_STORE 1
+#endif
+#if OTPU_GEMM_NT_STORE
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(f32x4{y[0], y[1], y[2], y[3]}, reinterpret_cast<f32x4*>(p));
+#else
+        *reinterpret_cast<float4*>(p) = make_float4(y[0], y[1], y[2], y[3]);
+#endif
+    }
+}
+
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int8_t* lds, const float* sa2, int m0, int n0,
                                               const v4i (&acc)[4][4], int sh) {
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -440,46 +493,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int8_t* lds, co
     const bool full = m0 + GBM <= a.M && n0 + GBN <= a.N;
     if (full && a.vec4) {
         int* T = reinterpret_cast<int*>(lds) + wid * 64 * TPS;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int t = 0; t < 4; ++t) T[(16 * i + 4 * (lane >> 4) + t) * TPS + 16 * j + (lane & 15)] = acc[i][j][t];
-        const int q = lane & 15, g = lane >> 4;
-        const int rt = (wid >> 1) * 64 + g;                      // the tile row of group s = 0
-        const int nc = n0 + (wid & 1) * 64 + 4 * q;
-        float sw[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) sw[c] = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(a.ws + (int64_t)(nc + c) * a.srs));
-        const bool asc = (a.flags & OTPU_ASCALE) != 0, accf = (a.flags & OTPU_ACC) != 0;
-#pragma unroll 2
-        for (int s = 0; s < 16; ++s) {
-            const int r = rt + 4 * s;
-            const int4 raw = *reinterpret_cast<const int4*>(T + (g + 4 * s) * TPS + 4 * q);
-            const float sa = sa2[r];
-            float y[4] = {ldexpf((float)raw.x, sh), ldexpf((float)raw.y, sh), ldexpf((float)raw.z, sh),
-                          ldexpf((float)raw.w, sh)};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) y[c] = fmul_f(fmul_f(y[c], sw[c]), sa);
-            float* p = a.out + (int64_t)(m0 + r) * a.ors + nc;
-            if (asc || accf) {
-                const float4 old = *reinterpret_cast<const float4*>(p);
-                const float o[4] = {old.x, old.y, old.z, old.w};
-                const float al = asc ? a.alpha[m0 + r] : 1.0f;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) y[c] = asc ? fadd(fmul(o[c], al), y[c]) : fadd(o[c], y[c]);
-            }
-#ifndef OTPU_GEMM_NT_STORE
-#define OTPU_GEMM_NT_STORE 1
-#endif
-#if OTPU_GEMM_NT_STORE
-            typedef float f32x4 __attribute__((ext_vector_type(4)));
-            __builtin_nontemporal_store(f32x4{y[0], y[1], y[2], y[3]}, reinterpret_cast<f32x4*>(p));
-#else
-            *reinterpret_cast<float4*>(p) = make_float4(y[0], y[1], y[2], y[3]);
-#endif
-        }
+        epi_transpose(T, acc);
+        epi_rows(a, T, sa2, m0, n0, wid, 0, 16, sh);
         return;
     }
     // a partial tile (or an unaligned output): each lane's own values, in the MFMA layout
@@ -899,11 +914,29 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
     const int np = __builtin_popcount(dmask);
     const bool mp = !single && plain && KT <= MP_KT && np >= 1 && np <= 2;
 
+    // a full tile's epilogue is shared: waves 0-3 write their transposes, then wave w and its
+    // loader w + 4 store 8 row groups each (one more barrier for both groups)
+    const bool split = m0 + GBM <= a.M && n0 + GBN <= a.N && a.vec4;
     if (fits && (single || mp)) {
         if (loader) {
             lw_load_walk(rs, KS);
+            if (split) {
+                __syncthreads();                         // the transposes written
+                const int w = wid & 3;
+                epi_rows(a, reinterpret_cast<const int*>(sRing) + w * 64 * TPS, sSa2, m0, n0, w, 8, 16, 16 - smax);
+            }
             return;
         }
+        auto epilogue = [&](const v4i (&acc0)[4][4]) {
+            if (split) {
+                int* T = reinterpret_cast<int*>(sRing) + wid * 64 * TPS;
+                epi_transpose(T, acc0);
+                __syncthreads();
+                epi_rows(a, T, sSa2, m0, n0, wid, 0, 8, 16 - smax);
+            } else {
+                tile_epilogue(a, sRing, sSa2, m0, n0, acc0, 16 - smax);
+            }
+        };
         int dv[MP_MAX];
         uint32_t left = dmask;
 #pragma unroll
@@ -919,7 +952,7 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
                 for (int j = 0; j < 4; ++j) acc[0][i][j] = v4i{0, 0, 0, 0};
             if (single) lw_mma_walk<1, false>(sRing, sDaAll, acc, dv, KS);
             else lw_mma_walk<1, true>(sRing, sDaAll, acc, dv, KS);
-            tile_epilogue(a, sRing, sSa2, m0, n0, acc[0], 16 - smax);
+            epilogue(acc[0]);
         } else {
             v4i acc[2][4][4];
 #pragma unroll
@@ -935,7 +968,7 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[0][i][j] = (acc[0][i][j] << (smax - dv[0])) + (acc[1][i][j] << (smax - dv[1]));
-            tile_epilogue(a, sRing, sSa2, m0, n0, acc[0], 16 - smax);
+            epilogue(acc[0]);
         }
         return;
     }
