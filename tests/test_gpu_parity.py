@@ -459,6 +459,30 @@ def test_gemm_acc_ascale(ops):
                                 old=old, alpha=alpha))
 
 
+@pytest.mark.parametrize("row_mode", [True, False])
+def test_gemm_acc_ascale_full_tiles(ops, row_mode):
+    """ACC (RSC weights) and ACC + ASCALE (UNIT weights: ASCALE needs both) through the
+    full-tile epilogue, whose rows the compute waves and the loader waves store half each:
+    128 x 384 outputs, three whole 128 x 128 tiles."""
+    _, _, mxu = ops
+    rng = np.random.default_rng(11)
+    M, N, K = 128, 384, 1024
+    x = spread(rng, M, K, 1.0, 32)
+    q, Sa, da = F.quantize_mx(x, 32, row_mode=row_mode)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    rows, srows = Q.pack_rsc(W)
+    old = rng.standard_normal((M, N)).astype(np.float32)
+    alpha = rng.standard_normal(M).astype(np.float32)
+    say("gemm acc / ascale, full tiles", "row" if row_mode else "mx")
+    got = mxu.mm(q, Sa, da, rows, srows, "int8", K, rsc=True, acc=old)
+    assert same_bits(got, OC.mm(q, Sa, da, rows, srows, "int8", K, flags=MM.RSC | MM.ACC, old=old))
+    wel = rng.integers(-127, 128, (N, K)).astype(np.int8).view(np.uint8)
+    zs = np.zeros((N, 8), np.uint8)
+    got = mxu.mm(q, Sa, da, wel, zs, "int8", K, unit=True, acc=old, alpha=alpha)
+    assert same_bits(got, OC.mm(q, Sa, da, wel, zs, "int8", K, flags=MM.UNIT | MM.ACC | MM.ASCALE,
+                                old=old, alpha=alpha))
+
+
 def test_gemm_c3_shape_tile_kinds(ops):
     """The c3 shape's kernel (loader waves beside the MFMA waves) on every kind of tile: each
     128-row tile's activation offsets drawn from its own set -- three planes (the masked passes,
