@@ -259,6 +259,8 @@ __device__ __forceinline__ void mfma_stage(const Smem& sm, int cur, v4i (&acc)[4
 }
 
 // one plane (d, e) over all of K: C += mask_d(A) . mask_e(B)^T in the int32 accumulators.
+// K / 128 + 1 barriers: gemm_lw_kernel's loader waves match them one for one
+// (masked_barriers), so a change to their number changes masked_barriers with it.
 // MA / MB: mask the activation groups by da == d / the weight blocks by dw == e (false: every
 // group of the tile is in the plane).  Rows past M or N are loaded from the last valid row
 // (no branches, no waits in the load path): they only reach outputs the epilogue skips.
@@ -551,7 +553,8 @@ __device__ __forceinline__ void gemm_tile_mp(const GemmArgs& a, int8_t* ring, co
     tile_epilogue(a, ring, sa2, m0, n0, acc[0], 16 - smax);
 }
 
-// a tile's planes in ascending s (Horner in the int32 accumulators), then its epilogue
+// a tile's planes in ascending s (Horner in the int32 accumulators), then its epilogue (its
+// (d, e) loop is masked_barriers' loop: keep the two the same)
 template <bool MA, bool MB>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int m0, int n0, uint32_t dmask,
                                           uint32_t emask, uint32_t smask, int smin, int smax, const float* sa2) {
