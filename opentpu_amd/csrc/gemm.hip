@@ -622,8 +622,10 @@ __device__ __forceinline__ void lw_load_walk(const RingSrc& rs, int KS) {
 
 // a compute wave's walk: NP planes into acc[p]; MASK: each stage's A fragments masked to plane
 // p's 32-groups (plain weights, offsets from da_lds as in gemm_pass_mp), else the single plane.
+// ALL1 (two planes covering every group): plane 1's product taken over every group instead,
+// C_all, so that only plane 0 is masked (C_1 = C_all - C_0 afterwards, exactly in int32).
 // KS + 1 barriers, matching lw_load_walk's.
-template <int NP, bool MASK>
+template <int NP, bool MASK, bool ALL1 = false>
 __device__ __forceinline__ void lw_mma_walk(const int8_t* ring, const uint32_t* da_lds, v4i (&acc)[NP][4][4],
                                             const int (&dv)[MP_MAX], int KS) {
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -654,7 +656,7 @@ __device__ __forceinline__ void lw_mma_walk(const int8_t* ring, const uint32_t* 
                 v4i fm[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const bool keep = !MASK || ((dw4[i] >> gsh) & 0xFFu) == (uint32_t)dv[p];
+                    const bool keep = !MASK || (ALL1 && p == 1) || ((dw4[i] >> gsh) & 0xFFu) == (uint32_t)dv[p];
                     fm[i] = keep ? fa[ks][i] : v4i{0, 0, 0, 0};
                 }
 #pragma unroll
@@ -964,13 +966,17 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) acc[p][i][j] = v4i{0, 0, 0, 0};
-            lw_mma_walk<2, true>(sRing, sDaAll, acc, dv, KS);
+            // (no offsets past the window: the two planes cover every group, so plane 1 is C_all)
+            if (!over) lw_mma_walk<2, true, true>(sRing, sDaAll, acc, dv, KS);
+            else lw_mma_walk<2, true>(sRing, sDaAll, acc, dv, KS);
             // sum_p C_p << (smax - d_p) (the bound checked above)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[0][i][j] = (acc[0][i][j] << (smax - dv[0])) + (acc[1][i][j] << (smax - dv[1]));
+                for (int j = 0; j < 4; ++j) {
+                    const v4i c1 = over ? acc[1][i][j] : acc[1][i][j] - acc[0][i][j];
+                    acc[0][i][j] = (acc[0][i][j] << (smax - dv[0])) + (c1 << (smax - dv[1]));
+                }
             epilogue(acc[0]);
         }
         return;
