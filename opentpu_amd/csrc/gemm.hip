@@ -446,18 +446,24 @@ __device__ __forceinline__ void epi_transpose(int* T, const v4i (&acc)[4][4]) {
             for (int t = 0; t < 4; ++t) T[(16 * i + 4 * (lane >> 4) + t) * TPS + 16 * j + (lane & 15)] = acc[i][j][t];
 }
 
-// row groups s0 .. s1 - 1 of region w's 16 (region w: the 64 x 64 of wave w) from T, scaled and
-// stored as 4-row x 256-byte float4 rows
-__device__ __forceinline__ void epi_rows(const GemmArgs& a, const int* T, const float* sa2, int m0, int n0, int w,
-                                         int s0, int s1, int sh) {
-    const int lane = threadIdx.x & 63;
+// this lane's 4 columns' Sw in region w's epilogue rows (1 with UNIT), as loaded: epi_rows
+// flushes them where it uses them, so that no wait for these loads comes before that
+__device__ __forceinline__ void epi_sw(const GemmArgs& a, int n0, int w, float (&sw)[4]) {
     const bool unit = (a.flags & OTPU_UNIT) != 0;
+    const int nc = n0 + (w & 1) * 64 + 4 * (threadIdx.x & 15);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sw[c] = unit ? 1.0f : *reinterpret_cast<const float*>(a.ws + (int64_t)(nc + c) * a.srs);
+}
+
+// row groups s0 .. s1 - 1 of region w's 16 (region w: the 64 x 64 of wave w) from T, scaled by
+// sw (epi_sw) and Sa and stored as 4-row x 256-byte float4 rows
+__device__ __forceinline__ void epi_rows(const GemmArgs& a, const int* T, const float* sa2, int m0, int n0, int w,
+                                         int s0, int s1, int sh, const float (&sw)[4]) {
+    const int lane = threadIdx.x & 63;
     const int q = lane & 15, g = lane >> 4;
     const int rt = (w >> 1) * 64 + g;                          // the tile row of group s = 0
     const int nc = n0 + (w & 1) * 64 + 4 * q;
-    float sw[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) sw[c] = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(a.ws + (int64_t)(nc + c) * a.srs));
+    const float swf[4] = {ftz(sw[0]), ftz(sw[1]), ftz(sw[2]), ftz(sw[3])};
     const bool asc = (a.flags & OTPU_ASCALE) != 0, accf = (a.flags & OTPU_ACC) != 0;
 #pragma unroll 2
     for (int s = s0; s < s1; ++s) {
@@ -467,7 +473,7 @@ __device__ __forceinline__ void epi_rows(const GemmArgs& a, const int* T, const 
         float y[4] = {ldexpf((float)raw.x, sh), ldexpf((float)raw.y, sh), ldexpf((float)raw.z, sh),
                       ldexpf((float)raw.w, sh)};
 #pragma unroll
-        for (int c = 0; c < 4; ++c) y[c] = fmul_f(fmul_f(y[c], sw[c]), sa);
+        for (int c = 0; c < 4; ++c) y[c] = fmul_f(fmul_f(y[c], swf[c]), sa);
         float* p = a.out + (int64_t)(m0 + r) * a.ors + nc;
         if (asc || accf) {
             const float4 old = *reinterpret_cast<const float4*>(p);
@@ -495,8 +501,10 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& a, int8_t* lds, co
     const bool full = m0 + GBM <= a.M && n0 + GBN <= a.N;
     if (full && a.vec4) {
         int* T = reinterpret_cast<int*>(lds) + wid * 64 * TPS;
+        float sw[4];
+        epi_sw(a, n0, wid, sw);
         epi_transpose(T, acc);
-        epi_rows(a, T, sa2, m0, n0, wid, 0, 16, sh);
+        epi_rows(a, T, sa2, m0, n0, wid, 0, 16, sh, sw);
         return;
     }
     // a partial tile (or an unaligned output): each lane's own values, in the MFMA layout
@@ -860,7 +868,14 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
     const int KT = a.K / GBK, KS = a.K / RBK;
 
     const RingSrc rs = ring_src(a, sRing, m0, n0);
+    // the epilogue's column scales, loaded early (a full tile's epilogue rows are shared by
+    // wave w and loader w + 4, region w & 3): a loader's before its ring loads, which complete
+    // in order after them (the stage waits' counts unchanged), a compute wave's after the
+    // offset scan (whose waits would otherwise wait for them too)
+    const bool split = m0 + GBM <= a.M && n0 + GBN <= a.N && a.vec4;
+    float esw[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     if (loader) {
+        if (split) epi_sw(a, n0, wid & 3, esw);
 #pragma unroll
         for (int s = 0; s < NS - 1; ++s)
             if (s < KS) ring_issue(rs, s);
@@ -900,6 +915,7 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
             sMask[2 * wid] = dm;
             sMask[2 * wid + 1] = em;
         }
+        if (split) epi_sw(a, n0, wid, esw);
     }
     __syncthreads();
     uint32_t dall = 0, eall = 0;
@@ -921,14 +937,13 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
 
     // a full tile's epilogue is shared: waves 0-3 write their transposes, then wave w and its
     // loader w + 4 store 8 row groups each (one more barrier for both groups)
-    const bool split = m0 + GBM <= a.M && n0 + GBN <= a.N && a.vec4;
     if (fits && (single || mp)) {
         if (loader) {
             lw_load_walk(rs, KS);
             if (split) {
                 __syncthreads();                         // the transposes written
                 const int w = wid & 3;
-                epi_rows(a, reinterpret_cast<const int*>(sRing) + w * 64 * TPS, sSa2, m0, n0, w, 8, 16, 16 - smax);
+                epi_rows(a, reinterpret_cast<const int*>(sRing) + w * 64 * TPS, sSa2, m0, n0, w, 8, 16, 16 - smax, esw);
             }
             return;
         }
@@ -937,7 +952,7 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
                 int* T = reinterpret_cast<int*>(sRing) + wid * 64 * TPS;
                 epi_transpose(T, acc0);
                 __syncthreads();
-                epi_rows(a, T, sSa2, m0, n0, wid, 0, 8, 16 - smax);
+                epi_rows(a, T, sSa2, m0, n0, wid, 0, 8, 16 - smax, esw);
             } else {
                 tile_epilogue(a, sRing, sSa2, m0, n0, acc0, 16 - smax);
             }
