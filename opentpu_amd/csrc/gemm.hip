@@ -593,6 +593,78 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& a, const Smem& sm, int
     tile_epilogue(a, sm.ring, sa2, m0, n0, acc, 16 - smax);
 }
 
+// The offsets present in a tile -- d over its activation rows, e over its weight rows, bit 17
+// for offsets past the window -- into sMask[2 w], sMask[2 w + 1] for each wave w of threads
+// 0-255, and the activation words into sDaAll (K <= 4096).  Packed offset rows (ldda = K / 32
+// bytes, 16-byte aligned, the tile's rows all present) are one contiguous block, read with
+// coalesced 16-byte loads: each line once.  Otherwise two threads a row read its words (each
+// load instruction then touches 64 rows' lines, and the tile's 64 lines are requested ~32 times
+// over: at the c3 shape that took the scan to 2.9 us, its requests queued among the ring's).
+__device__ __forceinline__ void tile_offsets(const GemmArgs& a, int m0, int n0, int KT, bool plain,
+                                             uint32_t* sDaAll, uint32_t* sMask) {
+    const int tid = threadIdx.x & 255, lane = tid & 63, wid = tid >> 6;
+    uint32_t dm = 0, em = 0;
+    auto take = [&](uint32_t wd) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t d = (wd >> (8 * t)) & 0xFF;
+            dm |= 1u << (d <= 16 ? d : 17);
+        }
+    };
+    const uint8_t* blk = a.da + (int64_t)m0 * a.ldda;
+    const bool packed = a.ldda == 4 * KT && (KT & 3) == 0 && ((uintptr_t)blk & 15) == 0 && m0 + GBM <= a.M;
+    if (packed) {
+        const uint4* v = reinterpret_cast<const uint4*>(blk);
+        const int NV = GBM * KT / 4;                     // 16-byte pieces of the tile's block
+        for (int i = tid; i < NV; i += 256) {
+            const uint4 q = v[i];
+            const int r = 4 * i / KT, k = 4 * i % KT;     // row r, words k .. k + 3
+            if (KT <= MP_KT) {
+                sDaAll[r * DAS + k] = q.x;
+                sDaAll[r * DAS + k + 1] = q.y;
+                sDaAll[r * DAS + k + 2] = q.z;
+                sDaAll[r * DAS + k + 3] = q.w;
+            }
+            take(q.x);
+            take(q.y);
+            take(q.z);
+            take(q.w);
+        }
+    } else {
+        const int r = tid & (GBM - 1), h = tid >> 7;
+        if (m0 + r < a.M) {
+            const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)(m0 + r) * a.ldda);
+#pragma unroll 8
+            for (int k = h; k < KT; k += 2) {             // K / 128 words of four offsets
+                const uint32_t wd = drow[k];
+                if (KT <= MP_KT) sDaAll[r * DAS + k] = wd;
+                take(wd);
+            }
+        }
+    }
+    if (plain) {
+        em = 1u;
+    } else {
+        const int r = tid & (GBN - 1), h = tid >> 7;
+        if (n0 + r < a.N) {
+            const uint8_t* wrow = a.ws + (int64_t)(n0 + r) * a.srs + 4 + a.k0;
+#pragma unroll 8
+            for (int k = h; k < KT; k += 2) {
+                const uint32_t e = wrow[k];
+                em |= 1u << (e <= 16 ? e : 17);
+            }
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        dm |= __shfl_xor(dm, o, 64);
+        em |= __shfl_xor(em, o, 64);
+    }
+    if (lane == 0) {
+        sMask[2 * wid] = dm;
+        sMask[2 * wid + 1] = em;
+    }
+}
+
 // the barriers gemm_tile<true, MB> executes: K / 128 + 1 for each (d, e) pass it makes
 __device__ __forceinline__ int masked_barriers(int KT, uint32_t dmask, uint32_t emask, uint32_t smask, int smin,
                                                int smax) {
@@ -724,43 +796,8 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmArgs a) {
 
     // the tile rows' Sa * 2^-16 for the epilogue (written before the scan's barrier)
     if (tid < GBM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-16)) : 0.0f;
-    // the offsets present in this tile: d over its activation rows, e over its weight rows.
-    // Two threads a row; the loads of a thread are independent (issued back to back).
-    {
-        uint32_t dm = 0, em = 0;
-        const int r = tid & (GBM - 1), h = tid >> 7;
-        if (m0 + r < a.M) {
-            const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)(m0 + r) * a.ldda);
-#pragma unroll 8
-            for (int k = h; k < KT; k += 2) {                 // K / 128 words of four offsets
-                const uint32_t wd = drow[k];
-                if (KT <= MP_KT) sDaAll[r * DAS + k] = wd;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint32_t d = (wd >> (8 * t)) & 0xFF;
-                    dm |= 1u << (d <= 16 ? d : 17);           // bit 17: a group beyond the window
-                }
-            }
-        }
-        if (plain) {
-            em = 1u;
-        } else if (n0 + r < a.N) {
-            const uint8_t* wrow = a.ws + (int64_t)(n0 + r) * a.srs + 4 + a.k0;
-#pragma unroll 8
-            for (int k = h; k < KT; k += 2) {
-                const uint32_t e = wrow[k];
-                em |= 1u << (e <= 16 ? e : 17);
-            }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-            dm |= __shfl_xor(dm, o, 64);
-            em |= __shfl_xor(em, o, 64);
-        }
-        if (lane == 0) {
-            sMask[2 * wid] = dm;
-            sMask[2 * wid + 1] = em;
-        }
-    }
+    // the offsets present in this tile
+    tile_offsets(a, m0, n0, KT, plain, sDaAll, sMask);
     __syncthreads();
     uint32_t dall = 0, eall = 0;
 #pragma unroll
@@ -881,40 +918,7 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
             if (s < KS) ring_issue(rs, s);
     } else {
         if (tid < GBM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-16)) : 0.0f;
-        // the offsets present in this tile, as gemm_i8_kernel finds them (waves 0-3)
-        uint32_t dm = 0, em = 0;
-        const int r = tid & (GBM - 1), h = tid >> 7;
-        if (m0 + r < a.M) {
-            const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)(m0 + r) * a.ldda);
-#pragma unroll 8
-            for (int k = h; k < KT; k += 2) {
-                const uint32_t wd = drow[k];
-                if (KT <= MP_KT) sDaAll[r * DAS + k] = wd;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint32_t d = (wd >> (8 * t)) & 0xFF;
-                    dm |= 1u << (d <= 16 ? d : 17);
-                }
-            }
-        }
-        if (plain) {
-            em = 1u;
-        } else if (n0 + r < a.N) {
-            const uint8_t* wrow = a.ws + (int64_t)(n0 + r) * a.srs + 4 + a.k0;
-#pragma unroll 8
-            for (int k = h; k < KT; k += 2) {
-                const uint32_t e = wrow[k];
-                em |= 1u << (e <= 16 ? e : 17);
-            }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-            dm |= __shfl_xor(dm, o, 64);
-            em |= __shfl_xor(em, o, 64);
-        }
-        if (lane == 0) {
-            sMask[2 * wid] = dm;
-            sMask[2 * wid + 1] = em;
-        }
+        tile_offsets(a, m0, n0, KT, plain, sDaAll, sMask);   // the offsets present in this tile
         if (split) epi_sw(a, n0, wid, esw);
     }
     __syncthreads();
