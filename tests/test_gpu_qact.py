@@ -253,12 +253,13 @@ def test_quantize_any_shape(ops, shape, axis):
 
 
 def test_lm_head_twice_on_one_best_buffer(ops):
-    """The running maximum is left zero by each call: a second call with other weights picks its
-    own token, not the first call's."""
+    """The running maximum is left zero by each call: a later call with other weights (and
+    another grid) picks its own token, not an earlier call's; the third call's best logit equals
+    the second's at a higher index, so a maximum left over would win the tie."""
     import torch
     X = ops[0]
     rng = np.random.default_rng(14)
-    N, K = 3000, 256
+    K = 256
     x = np.abs(rng.standard_normal((1, K))).astype(np.float32)
     q, Sa, da = F.quantize_mx(x, 32)
     best = torch.zeros((2,), dtype=torch.int64, device="cuda")
@@ -266,7 +267,7 @@ def test_lm_head_twice_on_one_best_buffer(ops):
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     qd, Sad, dad = d(q), d(Sa), d(da)
     say("lm head twice")
-    for hot, scale in ((2500, 0.05), (17, 0.01)):          # the second call's logits are smaller
+    for N, hot, scale in ((3000, 2500, 0.05), (1000, 17, 0.01), (3000, 2999, 0.01)):
         rows = rng.integers(-20, 21, (N, K)).astype(np.int8)
         rows[hot] = 127
         srows = np.full((N, 1), scale, np.float32).view(np.uint8)
