@@ -384,6 +384,12 @@ GEMM_CASES = [  # M, N, K, weights (rsc | int8x | unit), activations (row | mx |
     (200, 300, 1024, "rsc", "row", 0),       # single plane, ragged tiles
     (72, 136, 640, "unit", "row", 0),        # single plane, an odd number of K stages
     (16, 16, 128, "rsc", "row", 0),          # single plane, one K stage
+    (100, 200, 4096, "rsc", "mx", 0),        # 32 K stages, up to 5 offsets a tile: masked passes
+    (64, 200, 8192, "rsc", "mx", 0),         # 64 K stages (the loaders count the passes' barriers)
+    (300, 96, 4224, "int8x", "mx", 1),       # 33 K stages, weight planes, k0
+    (48, 130, 6144, "rsc", "row", 0),        # single plane, a long ring walk
+    (16, 8192, 256, "rsc", "row", 0),        # 64 column tiles: the XCD-major tile order
+    (17, 1000, 128, "unit", "mx", 0),        # one row past a tile, a ragged last column tile
 ]
 
 
@@ -414,21 +420,24 @@ def test_gemm(ops, M, N, K, wk, ak, k0):
     assert same_bits(got, want)
 
 
-@pytest.mark.parametrize("dset", [(0, 1), (0, 1, 2), (1, 3, 4), (0, 1, 2, 3), (0, 20), (2, 5, 17), (0, 31)])
-def test_gemm_activation_planes(ops, dset):
+@pytest.mark.parametrize("dset,K", [((0, 1), 1024), ((0, 1, 2), 1024), ((1, 3, 4), 1024), ((0, 1, 2, 3), 1024),
+                                    ((0, 20), 1024), ((2, 5, 17), 1024), ((0, 31), 1024),
+                                    ((0, 1), 4096), ((0, 2), 4224), ((1,), 8192)])
+def test_gemm_activation_planes(ops, dset, K):
     """Plain (RSC) weights x activation groups whose offsets take the values dset: one to three
     planes in one K walk, four planes in the plane-by-plane passes, offsets past the window
-    (dropped); against the C oracle."""
+    (dropped); two planes in one walk at 32 K stages (the staged offsets full) and in the
+    plane-by-plane passes at 33; one offset everywhere over 64 stages; against the C oracle."""
     import torch
     _, _, mxu = ops
-    rng = np.random.default_rng(sum(dset) * 7 + len(dset))
-    M, N, K = 200, 256, 1024
+    rng = np.random.default_rng(sum(dset) * 7 + len(dset) + K)
+    M, N = 200, 256
     q = rng.integers(-127, 128, (M, K)).astype(np.int8)
     Sa = np.abs(rng.standard_normal(M)).astype(np.float32) + np.float32(0.5)
     da = np.asarray(dset, np.uint8)[rng.integers(0, len(dset), (M, K // 32))]
     W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     rows, srows = Q.pack_rsc(W)
-    say("gemm planes", dset)
+    say("gemm planes", dset, K)
     got = mxu.mm(q, Sa, da, rows, srows, "int8", K, rsc=True)
     want = OC.mm(q, Sa, da, rows, srows, "int8", K, flags=MM.RSC)
     assert same_bits(got, want)
