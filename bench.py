@@ -144,7 +144,7 @@ def lm_head(steps, warmup):
     x = torch.randn((1, K), generator=gen, device="cuda")
     q, Sa, da = fp32.quantize_mx(x, 32)
     logits = torch.empty((N,), dtype=torch.float32, device="cuda")
-    best = torch.zeros((2,), dtype=torch.int64, device="cuda")      # result word, running maximum
+    best = torch.zeros((X.LM_STATE_BYTES // 8,), dtype=torch.int64, device="cuda")  # result word, maxima
     tok = torch.empty((1,), dtype=torch.int32, device="cuda")
 
     def step():

@@ -225,10 +225,13 @@ int otpu_mm_batched(int B, const int8_t* q, int64_t ldq, int64_t q_bstride, cons
 
 /* LM head + greedy: one activation row (M = 1) times N vocabulary rows, the logits' total-order
  * maximum with the first index (opentpu/llm/qwen3.py:2052-2088 + opentpu/llm/generate.py:251-286
- * + VOP ARGMAX opentpu/isasim.py:1141-1152).  best[0] = max over n of (key(y_n) << 32 |
- * ~(base+n)) (a u64 whose low word is the complement of the index); token = base + that n.
- * best[1] is the running maximum the GEMV's workgroups raise: zero before the first call (e.g.
- * allocated zeroed), and every call leaves it zero again.  logits may be NULL.  Two kernels. */
+ * + VOP ARGMAX opentpu/isasim.py:1141-1152).  best is the call's state, OTPU_LM_STATE_BYTES
+ * 16-byte aligned: best[0] = max over n of (key(y_n) << 32 | ~(base+n)) (a u64 whose low word
+ * is the complement of the index); token = base + that n.  The rest holds the running maxima
+ * the GEMV's workgroups raise: zero before the first call (e.g. allocated zeroed), and every
+ * call leaves it zero again.  Calls on one state must not overlap.  logits may be NULL.  Two
+ * kernels. */
+#define OTPU_LM_STATE_BYTES 16640  /* 64 maxima 256 bytes apart, after the result's 256 */
 int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8_t* da, int K,
                         const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N,
                         int fmt, int flags, int k0, int64_t base, float* logits,

@@ -18,6 +18,7 @@ FMT = {"int8": INT8, "int4": INT4, "fp4": FP4, "nvfp4": NVFP4}
 UNIT, ACC, RMAX, ASCALE, PAIR, RSC = 0x1, 0x2, 0x4, 0x8, 0x40, 0x80
 Q_ROW, Q_LO, Q_HL = 0x1, 0x10, 0x20             # QACT / QST flags
 QALIGN = 64                                     # QACT ST / LDA row alignment
+LM_STATE_BYTES = 16640                          # the LM head's state (result word, maxima)
 
 # every exported symbol and its argument types (P pointer, L int64, I int32, F float, D double)
 _P, _L, _I, _F, _D = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double

@@ -32,14 +32,16 @@ __global__ void sum_parts(const float* __restrict__ part, int64_t pstride, int R
     *o = y;
 }
 
-// the LM head's last step: the running maximum best[1] becomes the result best[0] and the
-// token, and is cleared for the next call (no fill launch before the GEMV)
-__global__ void best_finish(uint64_t* best, int32_t* token) {
+// the LM head's last step: the maximum over the running maxima (state[LM_STRIDE (1 + j)], one
+// a lane) becomes the result state[0] and the token; the maxima are cleared for the next call
+__global__ __launch_bounds__(64) void best_finish(uint64_t* state, int32_t* token) {
+    static_assert(LM_WORDS == 64, "one word a lane");
+    uint64_t* w = state + LM_STRIDE * (1 + threadIdx.x);
+    const uint64_t m = wave_max_u64(*w);
+    *w = 0;
     if (threadIdx.x == 0) {
-        const uint64_t b = best[1];
-        best[0] = b;
-        best[1] = 0;
-        *token = (int32_t)~(uint32_t)(b & 0xFFFFFFFFull);
+        state[0] = m;
+        *token = (int32_t)~(uint32_t)(m & 0xFFFFFFFFull);
     }
 }
 
@@ -387,10 +389,10 @@ extern "C" int otpu_lm_head_argmax(const int8_t* q, const float* Sa, const uint8
     if (rc) return rc;
     if (!Sa || !best || !token) return otpu_fail(OTPU_EINVAL, "lm_head_argmax: NULL Sa, best or token");
     if (base < 0 || base + (int64_t)N > 0xFFFFFFFFll) return otpu_fail(OTPU_EINVAL, "lm_head_argmax: base %lld", (long long)base);
-    if (!al(best, 16)) return otpu_fail(OTPU_EALIGN, "lm_head_argmax: best (two words) 16-byte aligned");
+    if (!al(best, 16)) return otpu_fail(OTPU_EALIGN, "lm_head_argmax: best (the state) 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     MMArgs a = make_args(q, K, Sa, da, K / 32, 1, K, w, rs, ws, srs, N, flags, k0);
-    a.out = logits; a.ors = N; a.best = best + 1; a.base = base;
+    a.out = logits; a.ors = N; a.best = best + LM_STRIDE; a.base = base;
     rc = launch_gemv(a, fmt, 1, s);
     if (rc) return rc;
     best_finish<<<1, 64, 0, s>>>(best, token);

@@ -7,6 +7,8 @@
 
 namespace otpu {
 
+constexpr int LM_WORDS = 64;      // the LM head's running maxima (one line each)
+constexpr int LM_STRIDE = 32;     // u64 words from one to the next (256 bytes)
 constexpr int LMAX = 8;            // pieces per lane held in registers (K <= 128 * LMAX * 16 / elements)
 
 struct MMArgs {
@@ -21,7 +23,8 @@ struct MMArgs {
     float* out; int64_t ors;
     uint32_t* rmax_key;            // RMAX: total-order keys, finished by rmax_finish
     int64_t* acc_out;              // exact accumulators instead of the epilogue
-    uint64_t* best;                // LM head: max of (key << 32 | ~index)
+    uint64_t* best;                // LM head: the maxima of (key << 32 | ~index), LM_WORDS words
+                                   // LM_STRIDE apart (workgroup b raises word b % LM_WORDS)
     int64_t base;                  // LM head: index of row 0
     int P, T;                      // 16-byte pieces per row, lanes per row (team)
     // batch strides (elements of each pointer's type; bytes for w / ws; blocks for k0)

@@ -671,7 +671,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             compute(st, n0);
         }
     }
-    if (a.best) {                               // one atomic per workgroup
+    if (a.best) {                               // one maximum a workgroup
         __shared__ uint64_t red[4];
         best = wave_max_u64(best);
         if (lane == 0) red[threadIdx.x >> 6] = best;
@@ -679,12 +679,13 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         if (threadIdx.x == 0) {
             uint64_t m = red[0];
             for (int i = 1; i < (int)(blockDim.x >> 6); ++i) m = red[i] > m ? red[i] : m;
-            // read the best word first and skip the atomic when it already holds more: the
-            // workgroups' atomics on one address serialize at the memory side, and once a large
-            // logit has landed most of them have nothing to add
-            auto* bp = reinterpret_cast<unsigned long long*>(a.best);
-            if (m && m > __hip_atomic_load(bp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-                __hip_atomic_fetch_max(bp, (unsigned long long)m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // an atomic max without return on one of LM_WORDS words, each on a line of its own:
+            // nothing waits for it (a test of the word first, or an atomic with return, would
+            // hold the workgroup's CU slot for a device-scope round trip), and the words spread
+            // the atomics, which serialize per line at the memory side
+            if (m)
+                __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(a.best) + LM_STRIDE * (blockIdx.x % LM_WORDS),
+                                       (unsigned long long)m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }

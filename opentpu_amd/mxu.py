@@ -92,7 +92,7 @@ def lm_head_argmax(q, Sa, da, rows, srows, fmt: str, K: int, *, rsc: bool = Fals
     wd, sd = X.dev(rows, np.uint8), X.dev(srows, np.uint8)
     N = wd.shape[0]
     lg = X.empty((N,), np.float32) if logits else None
-    best = X.zeros((2,), np.int64)                 # the result word, the running maximum (zero)
+    best = X.zeros((X.LM_STATE_BYTES // 8,), np.int64)   # the result word, the running maxima (zero)
     tok = X.empty((1,), np.int32)
     X.call("otpu_lm_head_argmax", X.ptr(qd), X.ptr(Sad), X.ptr(dad), K, X.ptr(wd), wd.shape[1], X.ptr(sd),
            sd.shape[1], N, X.FMT[fmt], _flags(rsc=rsc), k0, base, X.ptr(lg), X.ptr(best), X.ptr(tok),
