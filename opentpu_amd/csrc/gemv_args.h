@@ -7,6 +7,9 @@
 
 namespace otpu {
 
+// threads of every kernel over the GEMV bodies (their __launch_bounds__ and launches): a
+// constant, since blockDim.x is read from the dispatch packet with a load and a wait
+constexpr int GEMV_THREADS = 256;
 constexpr int LM_WORDS = 64;      // the LM head's running maxima (one line each)
 constexpr int LM_STRIDE = 32;     // u64 words from one to the next (256 bytes)
 constexpr int LMAX = 8;            // pieces per lane held in registers (K <= 128 * LMAX * 16 / elements)

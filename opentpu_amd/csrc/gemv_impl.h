@@ -485,43 +485,62 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
     uint32_t act[MR][L][AW];
     int shA[MR][L];
     float sa2[MR];
-    if constexpr (QIN) {
-        static_assert(MR == 1, "the prologue QACT quantizes one activation row");
-        // (quantized by qin_prologue below, once the first rows' loads are in flight)
-    } else {
+    static_assert(!QIN || MR == 1, "the prologue QACT quantizes one activation row");
+    // (QIN: quantized by qin_prologue below, once the first rows' loads are in flight.)
+    // Otherwise every activation load goes out at once (act_issue), then the first rows' weight
+    // loads, then the pieces are unpacked (act_finish, whose waits, the loads completing in order,
+    // do not cover the weights). A piece past P or a row past M reads piece 0 of row 0 and keeps
+    // it: its shift is made negative, which drops its terms (piece_term), so no branch or select
+    // sits between the loads (with a branch around each piece's loads, each offset byte's wait
+    // came before the next piece's loads and before any weight load).
+    constexpr int AQ = FMT == OTPU_INT8 ? 1 : 2;          // 16-byte loads a piece
+    uint4 araw[MR][L][AQ];
+    int draw[MR][L];
+    auto act_issue = [&] {
 #pragma unroll
-    for (int j = 0; j < MR; ++j) {
+        for (int j = 0; j < MR; ++j) {
 #pragma unroll
-        for (int i = 0; i < L; ++i) {
-            const int p = i * T + tl;
-            const bool ok = p < P && j < a.M;
-            if (FMT == OTPU_INT8) {
-                uint4 v = ok ? *reinterpret_cast<const uint4*>(q + j * a.ldq + 16 * p) : make_uint4(0, 0, 0, 0);
-                act[j][i][0] = v.x; act[j][i][1] = v.y; act[j][i][2] = v.z; act[j][i][3] = v.w;
-                shA[j][i] = W - (ok ? (int)da[j * a.ldda + (p >> 1)] : 0);
-            } else {
-                uint4 v0 = make_uint4(0, 0, 0, 0), v1 = v0;
-                if (ok) {
-                    v0 = *reinterpret_cast<const uint4*>(q + j * a.ldq + 32 * p);
-                    v1 = *reinterpret_cast<const uint4*>(q + j * a.ldq + 32 * p + 16);
-                }
-                const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            for (int i = 0; i < L; ++i) {
+                const int p = i * T + tl;
+                const bool ok = p < P && j < a.M;
+                const int8_t* qp = q + (ok ? j * a.ldq + 16 * AQ * p : 0);
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    act[j][i][2 * t] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x06040200u);
-                    act[j][i][2 * t + 1] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x07050301u);
-                }
-                shA[j][i] = W - (ok ? (int)da[j * a.ldda + p] : 0);
+                for (int h = 0; h < AQ; ++h) araw[j][i][h] = *reinterpret_cast<const uint4*>(qp + 16 * h);
+                draw[j][i] = da[ok ? j * a.ldda + (FMT == OTPU_INT8 ? (p >> 1) : p) : 0];
             }
         }
-    }
+    };
+    auto act_finish = [&] {
 #pragma unroll
-    for (int j = 0; j < MR; ++j) sa2[j] = (j < a.M && !a.acc_out) ? fmul(Sa[j], pow2f(-W)) : 0.0f;
-    }
+        for (int j = 0; j < MR; ++j) {
+#pragma unroll
+            for (int i = 0; i < L; ++i) {
+                const uint4 v0 = araw[j][i][0];
+                if (FMT == OTPU_INT8) {
+                    act[j][i][0] = v0.x; act[j][i][1] = v0.y; act[j][i][2] = v0.z; act[j][i][3] = v0.w;
+                } else {
+                    const uint4 v1 = araw[j][i][AQ - 1];
+                    const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        act[j][i][2 * t] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x06040200u);
+                        act[j][i][2 * t + 1] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x07050301u);
+                    }
+                }
+                const bool ok = i * T + tl < P && j < a.M;
+                shA[j][i] = ok ? W - draw[j][i] : -4096;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MR; ++j) sa2[j] = (j < a.M && !a.acc_out) ? fmul(Sa[j], pow2f(-W)) : 0.0f;
+    };
 
     // wave-uniform by construction; readfirstlane tells the compiler (scalar loop, no exec masks)
-    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
-    const int nwaves = (gridDim.x * blockDim.x) >> 6;
+    // (the launches' 256 threads as a constant; the persistent chain's phases keep blockDim.x,
+    // which measured ~3 us a step faster there)
+    const int nthr = LL ? (int)blockDim.x : GEMV_THREADS;
+    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * nthr + threadIdx.x) >> 6);
+    const int nwaves = (gridDim.x * nthr) >> 6;
     const int RW = R * NT;                      // rows a wave takes per iteration
     const int stride = nwaves * RW;
     uint64_t best = 0;
@@ -665,7 +684,16 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             compute(st, n0);
         }
     } else {
-        for (int n0 = wave * RW; n0 < a.N; n0 += stride) {
+        // the first rows stream in while the activation row loads
+        act_issue();
+        const int nfirst = wave * RW;
+        if (nfirst < a.N) {
+            Stage st;
+            load(st, nfirst);
+            act_finish();
+            compute(st, nfirst);
+        }
+        for (int n0 = nfirst + stride; n0 < a.N; n0 += stride) {
             Stage st;
             load(st, n0);
             compute(st, n0);
@@ -678,7 +706,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         __syncthreads();
         if (threadIdx.x == 0) {
             uint64_t m = red[0];
-            for (int i = 1; i < (int)(blockDim.x >> 6); ++i) m = red[i] > m ? red[i] : m;
+            for (int i = 1; i < GEMV_THREADS / 64; ++i) m = red[i] > m ? red[i] : m;
             // an atomic max without return on one of LM_WORDS words, each on a line of its own:
             // nothing waits for it (a test of the word first, or an atomic with return, would
             // hold the workgroup's CU slot for a device-scope round trip), and the words spread
