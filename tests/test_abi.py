@@ -38,3 +38,13 @@ def test_library_exports_every_declared_symbol():
         assert len(_lib.SIGNATURES[name][0]) == nargs, name
         assert fn is not None
     assert lib.otpu_version() >= 1
+
+
+def test_header_constants_match_the_binding():
+    """The sizes the header states (OTPU_QALIGN, OTPU_LM_STATE_BYTES) are the ones the Python
+    binding allocates with, and the LM head's state holds its 64 maxima 256 bytes apart after the
+    result's 256 bytes."""
+    src = open(os.path.join(ROOT, "include", "otpu.h")).read()
+    consts = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define (OTPU_\w+)\s+(\d+)", src)}
+    assert consts["OTPU_QALIGN"] == _lib.QALIGN
+    assert consts["OTPU_LM_STATE_BYTES"] == _lib.LM_STATE_BYTES == 256 * (1 + 64)
