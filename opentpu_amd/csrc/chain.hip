@@ -102,6 +102,20 @@ union ChainLds {
 #define OTPU_CHAIN_C4 1
 #endif
 
+// a field of the plan or of its layer table, read through the constant address space: the
+// plan does not change while a step runs (only what its pointers point to), and the compiler,
+// told so, reads it with scalar loads. Read as global memory after the step's first stores,
+// which it cannot prove do not alias the plan, every phase re-read its fields with vector
+// loads and waited for them before issuing its weights.
+template <typename T>
+__device__ __forceinline__ T cload(const T& r) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return *(const __attribute__((address_space(4))) T*)&r;
+#else
+    return r;                                    // (the host pass of this device code)
+#endif
+}
+
 // NORMS: 0 no RSCALE / CSCALE factors (constant NULLs), 1 some, 2 both in every layer (the
 // prologues' tests of the factors drop out)
 template <int FMT, bool FIXED, bool C4, int NORMS>
@@ -109,22 +123,24 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     constexpr int NRM = NORMS == 0 ? 1 : NORMS == 2 ? 2 : 0;    // the prologues' factor flag
     const int b = blockIdx.x;
     const uint32_t E = __hip_atomic_load(P.calls + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int NL = P.layers;
+    const int NL = cload(P.layers);
     const uint32_t t0 = E * (uint32_t)(4 * NL);
+    const ChainLayer* LY = cload(P.layer);
     for (int l = 0; l < NL; ++l) {
-        const ChainLayer& ly = P.layer[l];
+        const ChainLayer& ly = LY[l];
 #pragma unroll 1
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * l + k;
-            MMArgs a = P.kind[k];
+            MMArgs a = cload(P.kind[k]);
             // stamps: 0 phase start, 1 weights issued (the wait starts), 2 input row in, 3 QACT
             // done, 4 rows stored
-            a.stamp = P.stamps ? P.stamps + ((int64_t)i * gridDim.x + b) * 8 : nullptr;
+            uint64_t* const st = cload(P.stamps);
+            a.stamp = st ? st + ((int64_t)i * gridDim.x + b) * 8 : nullptr;
             OTPU_STAMP(a, 0);
             if (b * rows_per_wg(k) >= a.N) continue;     // no rows here: nothing to wait for
-            a.w = ly.w[k];
-            a.ws = ly.ws[k];
-            a.out = ly.out[k];
+            a.w = cload(ly.w[k]);
+            a.ws = cload(ly.ws[k]);
+            a.out = cload(ly.out[k]);
             // what every chain phase shares, as constants (their branches drop out of the code):
             // weights with scale rows from block 0, one input row, no VOP MUL, no batch
             a.flags = 0;
@@ -137,23 +153,24 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             a.rmax_key = nullptr;
             a.q_bs = a.sa_bs = a.da_bs = a.w_bs = a.ws_bs = a.out_bs = a.xin_bs = 0;
             a.k0_bs = 0;
-            a.ll_in = i ? P.ll[(i - 1) % 3] : nullptr;
-            a.xin = P.x0;
-            a.ll_out = P.ll[i % 3];
+            a.ll_in = i ? cload(P.ll[(i - 1) % 3]) : nullptr;
+            a.xin = cload(P.x0);
+            a.ll_out = cload(P.ll[i % 3]);
             a.tag_in = t0 + (uint32_t)i;
             a.tag_out = t0 + (uint32_t)i + 1;
-            a.err = P.err;
-            a.spin = FIXED ? CHAIN_SPIN : P.spin;
+            a.err = cload(P.err);
+            a.spin = FIXED ? CHAIN_SPIN : cload(P.spin);
             a.ll_all = 0;
             a.rscale = nullptr;                          // (o and the fold have none)
             a.cscale = nullptr;
             if (NORMS != 0 && (k == 0 || k == 2)) {
-                a.rscale = P.rnorm ? P.rnorm + 2 * l + (k >> 1) : nullptr;
-                a.cscale = ly.cs[k >> 1];
+                const float* const rn = cload(P.rnorm);
+                a.rscale = rn ? rn + 2 * l + (k >> 1) : nullptr;
+                a.cscale = cload(ly.cs[k >> 1]);
             }
             // (C4: 4-bit rows of K / 2 bytes, scale rows of 8 + 8 ceil(K / 256) bytes)
             if (k == 1) {
-                if (P.kv_wait) a.ll_all = P.kind[0].N;       // o waits for k and v too
+                if (cload(P.kv_wait)) a.ll_all = cload(P.kind[0].N);   // o waits for k and v too
                 if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; a.rs = 1024; a.srs = 72; }
                 gemv_body<FMT, 1, 1, O_T, false, true, O_R, true, true, 1>(a, &lds.q);
             } else if (k == 3) {
