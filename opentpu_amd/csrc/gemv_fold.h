@@ -87,9 +87,8 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
     // (workgroups of 256 threads: the mask tells the compiler so, and the chunk tests below then
     // resolve at compile time where K is a constant)
     const int tid = threadIdx.x & 255, lane = tid & 63, tl = lane & (T - 1), team = lane / T;
-    const int nthr = LL ? (int)blockDim.x : GEMV_THREADS;          // (as in gemv_body)
-    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * nthr + tid) >> 6);
-    const int nwaves = (gridDim.x * nthr) >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * GEMV_THREADS + tid) >> 6);
+    const int nwaves = (gridDim.x * GEMV_THREADS) >> 6;
     const float* x = a.xin;
     const float* xm = a.xmul;
 

@@ -536,11 +536,8 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
     };
 
     // wave-uniform by construction; readfirstlane tells the compiler (scalar loop, no exec masks)
-    // (the launches' 256 threads as a constant; the persistent chain's phases keep blockDim.x,
-    // which measured ~3 us a step faster there)
-    const int nthr = LL ? (int)blockDim.x : GEMV_THREADS;
-    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * nthr + threadIdx.x) >> 6);
-    const int nwaves = (gridDim.x * nthr) >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane((blockIdx.x * GEMV_THREADS + threadIdx.x) >> 6);
+    const int nwaves = (gridDim.x * GEMV_THREADS) >> 6;
     const int RW = R * NT;                      // rows a wave takes per iteration
     const int stride = nwaves * RW;
     uint64_t best = 0;
