@@ -175,7 +175,12 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
                 gemv_body<FMT, 1, 1, O_T, false, true, O_R, true, true, 1>(a, &lds.q);
             } else if (k == 3) {
                 if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; a.rs = 1536; a.srs = 104; }
+                // the next layer's table line read into the scalar cache during the fold, so that
+                // its first phase finds its weight pointers there (the empty asm keeps the load;
+                // its wait falls after the fold's own waits): ~1.5 us a step
+                const uint8_t* const next = cload(LY[l + 1 < NL ? l + 1 : l].w[0]);
                 fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
+                asm volatile("" ::"s"(next));
             } else if (C4 && k == 0) {                   // (its own call site: its constants)
                 if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 4096; a.gu_pair = 0; a.rs = 512; a.srs = 40; }
                 if (i == 0) gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, false, NRM>(a, &lds.q);   // plain x0
