@@ -731,20 +731,20 @@ __global__ __launch_bounds__(256) void gemv_qin_kernel(MMArgs a) {
     else gemv_body<FMT, 1, L, 16, PLAIN, true, R>(a);
 }
 
-// workgroups per CU the streaming grid aims for (measured on MI355X): for one piece a lane 40
-// with 4-bit weights (the 80-problem c2: 6.71-6.72 against 6.66-6.69 TB/s at 32 and 6.67-6.71
-// at 44 over four paired runs, 6.36 at 16, 6.50-6.79 at 64; each wave streams one or two row
-// groups, so the last round of workgroups is short) and 64 with int8 (the 128-problem c1:
-// 6.86-6.92 against 6.59-6.62 TB/s at 32, one row group a wave); 24 for four or more pieces (the LM head: 103.7-104.4
-// against 104.6-106.5 us at 16 over four paired runs, 106-108 at 8, 12 or 32), else 8;
-// OTPU_GEMV_BLOCKS_PER_CU overrides
+// workgroups per CU the streaming grid aims for (measured on MI355X): for one piece a lane 64,
+// where the 80-problem c2 and the 128-problem c1 give each wave one row group (c2: 7.01-7.03
+// TB/s against 6.58-6.79 at 40, 6.74-6.83 at 32, 6.80-6.82 at 48 and 6.90 at 56, two runs on
+// one box; c1: 6.86-6.92 against 6.59-6.62 at 32); 24 for four or more pieces (the LM head:
+// 103.7-104.4 against 104.6-106.5 us at 16 over four paired runs, 106-108 at 8, 12 or 32),
+// else 8; OTPU_GEMV_BLOCKS_PER_CU overrides
 inline int gemv_blocks_per_cu(int L, int fmt) {
+    (void)fmt;
     static const int v = [] {                   // read once (thread-safe static initialisation)
         const char* e = getenv("OTPU_GEMV_BLOCKS_PER_CU");
         const int x = e ? atoi(e) : 0;
         return (x > 0 && x <= 64) ? x : 0;
     }();
-    return v ? v : (L == 1 ? (fmt == OTPU_INT8 ? 64 : 40) : (L >= 4 ? 24 : 8));
+    return v ? v : (L == 1 ? 64 : (L >= 4 ? 24 : 8));
 }
 
 // rows a team takes per iteration (one activation row, one piece a lane) when the default
