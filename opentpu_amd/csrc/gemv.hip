@@ -36,6 +36,7 @@ __global__ void sum_parts(const float* __restrict__ part, int64_t pstride, int R
 // a lane) becomes the result state[0] and the token; the maxima are cleared for the next call
 __global__ __launch_bounds__(64) void best_finish(uint64_t* state, int32_t* token) {
     static_assert(LM_WORDS == 64, "one word a lane");
+    static_assert(8 * LM_STRIDE * (1 + LM_WORDS) == OTPU_LM_STATE_BYTES, "the state's size in otpu.h");
     uint64_t* w = state + LM_STRIDE * (1 + threadIdx.x);
     const uint64_t m = wave_max_u64(*w);
     *w = 0;
