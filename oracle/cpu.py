@@ -24,7 +24,17 @@ def lib():
         _lib.otpu_cpu_mm.argtypes = [P, L, P, P, L, I, I, P, L, P, L, I, I, I, I, P, P, L, P, P]
         _lib.otpu_cpu_argmax.argtypes = [P, L, P, P]
         _lib.otpu_cpu_threads.argtypes = [I]
+        _lib.otpu_cpu_recip.argtypes = [P, L, P]
+        _lib.otpu_cpu_recip.restype = None
     return _lib
+
+
+def recip(x):
+    """The C restatement's recip, elementwise (float32 in, float32 out)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().otpu_cpu_recip(_p(x), x.size, _p(y))
+    return y
 
 
 def _p(a):

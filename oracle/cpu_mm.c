@@ -72,6 +72,13 @@ int otpu_cpu_threads(int n) {
 #endif
 }
 
+/* recip of n values: the C restatement's own recip, exported so that the tests can check it
+ * against the reference's golden vectors directly (QACT's bytes rarely show a one-ulp slip). */
+void otpu_cpu_recip(const float* x, long n, float* y) {
+    #pragma omp parallel for schedule(static)
+    for (long i = 0; i < n; ++i) y[i] = recip(x[i]);
+}
+
 /* quantize_mx of M rows of K: q int8 [M, ldq], S [M], d [M, ldd] (K/g offsets a row). */
 int otpu_cpu_qact(const float* x, int M, int K, long ldx, int g, int row_mode,
                   int8_t* q, long ldq, float* S, uint8_t* d, long ldd) {
