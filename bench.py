@@ -211,6 +211,8 @@ def c4_step(steps, warmup, persistent=True):
         chains[it[0] % 2].step()
         it[0] += 1
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    for c in chains:                    # a step whose hand-off waits gave up is no measurement
+        c.check()
     wb = sh.layers * sh.layer_bytes("int4")
     launches = chains[0].kernels_per_step
     del chains

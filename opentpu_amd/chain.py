@@ -262,13 +262,33 @@ class DecodeChain:
         return ptr
 
     def chain_error(self) -> int:
-        """The persistent plan's error word (0: every hand-off of every step so far completed)."""
+        """The persistent plan's error word (0: every hand-off of every step so far completed).
+        It reads device memory: call it after the steps it covers have finished."""
         if self._plan is None:
             return 0
         import ctypes as C
         e = C.c_uint32(0)
         X.call("otpu_chain_error", self._plan[1], C.byref(e))
         return int(e.value)
+
+    def check(self) -> None:
+        """Wait for the queued steps and raise OtpuError if a hand-off wait of the persistent
+        step gave up (its workgroups were not all resident, e.g. CUs held by other work): the
+        outputs of that step and of every later one are then invalid.  The word is sticky: a
+        chain that failed stays failed (build a new DecodeChain).  The reference's simulator
+        raises on a wait that can never hold (`opentpu/isasim.py:1383-1397`)."""
+        if self._plan is None:
+            return
+        X.torch().cuda.synchronize()
+        e = self.chain_error()
+        if e:
+            raise X.OtpuError(X.OTPU_ETIMEOUT, f"chain step: a hand-off wait timed out (error word {e}); "
+                              "the step's outputs are invalid")
+
+    @staticmethod
+    def _capturing() -> bool:
+        T = X.torch()
+        return bool(T.cuda.is_current_stream_capturing())
 
     @property
     def kernels_per_step(self) -> int:
@@ -306,12 +326,16 @@ class DecodeChain:
             self.layer(l, src, dst)
             src = dst
 
-    def step(self, x=None):
+    def step(self, x=None, check: bool = True):
         """One decode step on input x [1, hidden] (fp32; default: the last input set):
-        returns the device tensor holding the last layer's output."""
+        returns the device tensor holding the last layer's output.  check (the persistent step,
+        outside a graph capture): wait for the step and raise OtpuError if a hand-off wait gave up
+        (`check`); check=False queues it without waiting, and the caller calls check() later."""
         if x is not None:
             self.x.copy_(X.dev(x, np.float32).reshape(1, -1))
         self._queue()
+        if check and self._plan is not None and not self._capturing():
+            self.check()
         return self.y
 
     def capture(self) -> None:
@@ -320,15 +344,19 @@ class DecodeChain:
         T = X.torch()
         self._queue()                                     # warm-up outside the capture
         T.cuda.synchronize()
+        self.check()
         g = T.cuda.CUDAGraph()
         with T.cuda.graph(g):
             self._queue()
         self._graph = g
 
-    def replay(self, x=None):
+    def replay(self, x=None, check: bool = True):
+        """Replay the captured step on x (default: the current self.x).  check: as in step()."""
         if self._graph is None:
             self.capture()
         if x is not None:
             self.x.copy_(X.dev(x, np.float32).reshape(1, -1))
         self._graph.replay()
+        if check and self._plan is not None:
+            self.check()
         return self.y

@@ -7,7 +7,7 @@
 static thread_local char g_err[512] = "";
 
 extern "C" const char* otpu_last_error(void) { return g_err; }
-extern "C" int otpu_version(void) { return 1; }
+extern "C" int otpu_version(void) { return OTPU_ABI_VERSION; }
 
 int otpu_fail(int code, const char* fmt, ...) {
     va_list ap;

@@ -242,6 +242,42 @@ static ChainLayout chain_layout(int layers, int maxn) {
 
 using namespace otpu;
 
+// The step's dynamic LDS: one workgroup a CU (the padding leaves room for no second; without it
+// the workgroups are resident all the same, some sharing a CU).
+static int chain_pad() {
+    static const int pad = [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(chain_kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, CHAIN_PAD_LDS) == hipSuccess
+                   ? CHAIN_PAD_LDS : 0;
+    }();
+    return pad;
+}
+
+// The step's workgroups wait on each other's rows, so all of them must be resident at once: the
+// occupancy the compiled kernel allows with its LDS, times the CUs, must cover the grid of one
+// workgroup a CU.  Checked once per device (the kernel's resources do not change); a device where
+// it does not hold refuses plans and steps instead of running into the waits' time-out.
+static int chain_resident_check(const char* what) {
+    static int cache[64] = {0};                          // 0 unknown, 1 fits, -1 does not
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return otpu_fail(OTPU_ENODEV, "%s: no current device", what);
+    int v = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+    int per_cu = 0;
+    if (v == 0) {
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(chain_kernel), 256, chain_pad());
+        if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "%s: occupancy query: %s", what, hipGetErrorString(e));
+        v = (int64_t)per_cu * otpu_cu_count() >= otpu_cu_count() ? 1 : -1;
+        __atomic_store_n(&cache[dev], v, __ATOMIC_RELAXED);
+    }
+    if (v < 0)
+        return otpu_fail(OTPU_ELAUNCH,
+                         "%s: the persistent step's %d workgroups cannot all be resident at once on this "
+                         "device (%d a CU); use the launch-per-linear path", what, otpu_cu_count(), per_cu);
+    return OTPU_OK;
+}
+
 extern "C" int64_t otpu_chain_plan_bytes(int layers, int hidden, int q_dim, int kv_dim, int F) {
     if (layers < 1 || hidden < 1 || q_dim < 1 || kv_dim < 0 || F < 1) return -1;
     const int maxn = std::max(std::max(q_dim + 2 * kv_dim, hidden), 2 * F);
@@ -267,6 +303,7 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
         return otpu_fail(OTPU_EINVAL, "chain_plan: %lld bytes, the plan needs %lld", (long long)plan_bytes,
                          (long long)lay.total);
     if (otpu_cu_count() > CHAIN_SLOTS) return otpu_fail(OTPU_EINVAL, "chain_plan: more than %d CUs", CHAIN_SLOTS);
+    if (int rc = chain_resident_check("chain_plan")) return rc;
     // each phase kind checked and built as its one-launch entry point would (layer 0's
     // pointers); then every layer's pointers checked the same way
     const int Ns[4] = {nq, hidden, 2 * F, hidden}, Ks[4] = {hidden, q_dim, hidden, F};
@@ -346,14 +383,9 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
 
 extern "C" int otpu_chain_step(const void* plan, otpu_stream_t stream) {
     if (!plan || (uintptr_t)plan % 256) return otpu_fail(OTPU_EINVAL, "chain_step: plan NULL or misaligned");
-    // one workgroup a CU (the padding LDS leaves room for no second; without it the workgroups
-    // are resident all the same, some sharing a CU)
-    static const int pad = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(chain_kernel),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, CHAIN_PAD_LDS) == hipSuccess
-                   ? CHAIN_PAD_LDS : 0;
-    }();
-    chain_kernel<<<(unsigned)otpu_cu_count(), 256, pad, (hipStream_t)stream>>>(static_cast<const ChainPlan*>(plan));
+    if (int rc = chain_resident_check("chain_step")) return rc;
+    chain_kernel<<<(unsigned)otpu_cu_count(), 256, chain_pad(), (hipStream_t)stream>>>(
+        static_cast<const ChainPlan*>(plan));
     return otpu_launch_check("chain_step");
 }
 

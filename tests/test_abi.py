@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
         assert name in _lib.SIGNATURES, name
         assert len(_lib.SIGNATURES[name][0]) == nargs, name
         assert fn is not None
-    assert lib.otpu_version() >= 1
+    assert lib.otpu_version() == _lib.ABI_VERSION
 
 
 def test_header_constants_match_the_binding():
@@ -47,4 +47,5 @@ def test_header_constants_match_the_binding():
     src = open(os.path.join(ROOT, "include", "otpu.h")).read()
     consts = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define (OTPU_\w+)\s+(\d+)", src)}
     assert consts["OTPU_QALIGN"] == _lib.QALIGN
+    assert consts["OTPU_ABI_VERSION"] == _lib.ABI_VERSION
     assert consts["OTPU_LM_STATE_BYTES"] == _lib.LM_STATE_BYTES == 256 * (1 + 64)

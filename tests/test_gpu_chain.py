@@ -435,6 +435,7 @@ def test_chain_wait_timeout_sets_the_error_word(X, monkeypatch):
     ends (every wave exits) and the plan's error word says the outputs are invalid; a plan with
     the default limit on the same chain then runs clean and bit-exact."""
     import torch
+    from opentpu_amd._lib import OtpuError
     from opentpu_amd.chain import DecodeChain, Shape
     sh = Shape(hidden=256, q_dim=512, kv_dim=256, F=768, layers=4)
     base = DecodeChain.synthetic(sh, "int4", seed0=31, std=0.05)
@@ -444,9 +445,15 @@ def test_chain_wait_timeout_sets_the_error_word(X, monkeypatch):
     ch = DecodeChain(base.layers, sh, "int4")
     say("chain timeout: spin 0")
     for _ in range(3):
-        ch.step(x)
+        ch.step(x, check=False)
     torch.cuda.synchronize()
     assert ch.chain_error() == 1
+    with pytest.raises(OtpuError, match="timed out"):       # the checked paths raise
+        ch.check()
+    with pytest.raises(OtpuError, match="timed out"):
+        ch.step(x)
+    with pytest.raises(OtpuError, match="timed out"):
+        ch.replay(x)
     monkeypatch.delenv("OTPU_CHAIN_SPIN")
     ok = DecodeChain(base.layers, sh, "int4")
     assert same_bits(ok.step(x).cpu().numpy(), want)
