@@ -19,6 +19,7 @@ UNIT, ACC, RMAX, ASCALE, PAIR, RSC = 0x1, 0x2, 0x4, 0x8, 0x40, 0x80
 Q_ROW, Q_LO, Q_HL = 0x1, 0x10, 0x20             # QACT / QST flags
 QALIGN = 64                                     # QACT ST / LDA row alignment
 LM_STATE_BYTES = 16640                          # the LM head's state (result word, maxima)
+ABI_VERSION = 2                                 # include/otpu.h OTPU_ABI_VERSION this binding follows
 
 # every exported symbol and its argument types (P pointer, L int64, I int32, F float, D double)
 _P, _L, _I, _F, _D = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double
@@ -55,9 +56,13 @@ SIGNATURES = {
     "otpu_sample": ([_P, _I, _P, _P, _D, _I, _F, _F, _P, _I, _P, _P, _P, _P], _I),
     "otpu_sample_static": ([_P, _I, _P, _P, _D, _I, _F, _F, _P, _I, _P, _P, _P], _I),
     "otpu_fake_act": ([_P, _I, _I, _L, _I, _I, _I, _P, _L, _P, _L, _P], _I),
+    "otpu_fake_act_f64": ([_P, _I, _I, _L, _I, _I, _I, _P, _L, _P, _L, _P], _I),
     "otpu_dequant": ([_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P], _I),
     "otpu_mx_matmul": ([_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P, _L, _P], _I),
 }
+
+
+OTPU_ETIMEOUT = -6         # the binding's own code: the persistent step's error word was set
 
 
 class OtpuError(RuntimeError):
@@ -83,6 +88,9 @@ def load(path: str = LIB_PATH):
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = res
+        if lib.otpu_version() != ABI_VERSION:
+            raise RuntimeError(f"{path} has ABI version {lib.otpu_version()}, this binding follows "
+                               f"{ABI_VERSION}: rebuild it (python -m opentpu_amd.build)")
         _lib = lib
     return _lib
 
