@@ -166,7 +166,9 @@ def lm_head(steps, warmup):
         pick()
     ms_both = timed(both, steps, warmup, torch.cuda.current_stream())
     sm.check()
-    return ms, int(tok.item()), ms_pick, ms_both
+    step()                                          # the logits and token of the LM head alone
+    sample = tuple(t.cpu().numpy() for t in (q, Sa, da, rows, srows, logits)) + (int(tok.item()),)
+    return ms, int(tok.item()), ms_pick, ms_both, sample
 
 
 def gemm(steps, warmup, row_mode=True):
@@ -187,7 +189,9 @@ def gemm(steps, warmup, row_mode=True):
     def step():
         X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, M, K, X.ptr(rows), K, X.ptr(srows), 4, N,
                X.FMT["int8"], X.RSC, 0, None, X.ptr(out), N, None, X.stream())
-    return timed(step, steps, warmup, torch.cuda.current_stream())
+    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    sample = tuple(t.cpu().numpy() for t in (q, Sa, da, rows, srows, out))
+    return ms, sample
 
 
 def c4_step(steps, warmup, persistent=True):
@@ -293,45 +297,110 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(sample, seconds=10.0):
-    """The C oracle (OpenMP) on this host, on the timed workload's first problem (its weights,
-    activation row and the GPU's output copied back from the device): one c2 GEMV repeated for
-    about `seconds` on min(16, cores) threads, its output checked against the GPU's bit for
-    bit; beside it (in `also`) the same C code on one thread and the numpy oracle (float64
-    group sums, the reference simulator's method), each on a few calls."""
+def _per_call(fn, seconds, max_reps):
+    """Seconds per call of fn, over about `seconds` (at least one call after a first one)."""
+    t0 = time.perf_counter()
+    fn()
+    one = time.perf_counter() - t0
+    reps = max(1, min(max_reps, int(seconds / max(one, 1e-5))))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def _same(a, b) -> bool:
+    a, b = np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
+
+
+def c4_layer_sample():
+    """One c4 layer (the decode step's first layer, weights seeded 100) on the GPU (the
+    persistent step, one layer) with host copies of its weights and input, for the CPU leg."""
+    import torch
+
+    from opentpu_amd.chain import DecodeChain, Shape
+    sh = Shape(layers=1)
+    ch = DecodeChain.synthetic(sh, "int4", seed0=100)
+    x = torch.randn((1, sh.hidden), generator=torch.Generator(device="cuda").manual_seed(4), device="cuda")
+    y = ch.step(x).cpu().numpy()
+    wts = {k: (r.cpu().numpy(), sr.cpu().numpy()) for k, (r, sr) in ch.layers[0].items()}
+    out = (x.cpu().numpy(), wts, y, sh)
+    del ch
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(samples, seconds=10.0):
+    """The C oracle (OpenMP) on this host, timed beside each config on its own workload, each
+    output checked against the GPU's bit for bit.  value: c2, the headline's problem 0 (one GEMV
+    repeated for about `seconds`) on min(16, cores) threads; `also`: c2 on one thread and in the
+    numpy oracle (float64 group sums, the reference simulator's method), then c1 (problem 0 of
+    its timed launch), c3 ROW (the whole GEMM; one thread: its first 64 rows), one c4 layer (QACT
+    and MM in the chain's order: q/k/v, o, gate/up, the 12 F-chunks of down) and c5 (the whole LM
+    head and its greedy token), each on all threads and on one."""
+    from oracle import chain as OCH
     from oracle import cpu as OC
     from oracle import mm as MM
     threads = min(16, os.cpu_count() or 1)
     OC.threads(threads)
     N, K = 6144, 2048
-    rows, srows, q, Sa, da, gpu_out = (t.cpu().numpy() for t in sample)
+    rows, srows, q, Sa, da, gpu_out = samples["c2"]
     q, Sa, da, gpu_out = q[:1], Sa[:1], da[:1], gpu_out[:1]
-    t0 = time.perf_counter()
     want = OC.mm(q, Sa, da, rows, srows, "int4", K)
-    one = time.perf_counter() - t0
-    matches = bool(np.array_equal(want.view(np.uint32), gpu_out.view(np.uint32)))
-    reps = max(1, min(2000, int(seconds / max(one, 1e-4))))
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        OC.mm(q, Sa, da, rows, srows, "int4", K)
-    dt = (time.perf_counter() - t0) / reps
+    matches = _same(want, gpu_out)
+    dt, reps = _per_call(lambda: OC.mm(q, Sa, da, rows, srows, "int4", K), seconds, 2000)
     OC.threads(1)
-    t0 = time.perf_counter()
-    for _ in range(20):
-        OC.mm(q, Sa, da, rows, srows, "int4", K)
-    dt1 = (time.perf_counter() - t0) / 20
+    dt1, _ = _per_call(lambda: OC.mm(q, Sa, da, rows, srows, "int4", K), 0.2, 20)
     OC.threads(threads)
     t0 = time.perf_counter()
     for _ in range(3):
         MM.mm(q, Sa, da, rows, srows, "int4", K)
     dtn = (time.perf_counter() - t0) / 3
+    also = {"c2": {"one_core": {"GBps": round(c2_bytes() / dt1 / 1e9, 3), "ms": round(dt1 * 1e3, 2)},
+                   "numpy_oracle": {"GBps": round(c2_bytes() / dtn / 1e9, 3), "ms": round(dtn * 1e3, 1)}},
+            "host_cores": os.cpu_count(), "threads": threads}
+
+    def both(name, fn, fn1, unit_of, what):
+        """fn on every thread (~2 s), fn1 (a smaller sample where named) on one; unit_of(dt, one)."""
+        dta, ra = _per_call(fn, 2.0, 200)
+        OC.threads(1)
+        dto, ro = _per_call(fn1, 1.0, 20)
+        OC.threads(threads)
+        also[name] = {"what": what, "all_cores": {**unit_of(dta, False), "ms": round(dta * 1e3, 3), "calls": ra},
+                      "one_core": {**unit_of(dto, True), "ms": round(dto * 1e3, 3), "calls": ro}}
+
+    if "c1" in samples:
+        r1, s1, q1, S1, d1, o1 = samples["c1"]
+        f1 = lambda: OC.mm(q1, S1, d1, r1, s1, "int8", 1024, flags=MM.RSC)   # noqa: E731
+        both("c1", f1, f1, lambda dt, one: {"GBps": round(c1_bytes() / dt / 1e9, 3)},
+             "int8 RSC GEMV 4096x1024 (problem 0 of the timed launch)")
+        also["c1"]["gpu_output_matches"] = _same(f1(), o1)
+    if "c3" in samples:
+        q3, S3, d3, r3, s3, o3 = samples["c3"]
+        f3 = lambda: OC.mm(q3, S3, d3, r3, s3, "int8", 2048, flags=MM.RSC)   # noqa: E731
+        f31 = lambda: OC.mm(q3[:64], S3[:64], d3[:64], r3, s3, "int8", 2048, flags=MM.RSC)  # noqa: E731
+        both("c3", f3, f31, lambda dt, one: {"TOPS": round(2 * (64 if one else 512) * 8192 * 2048 / dt / 1e12, 4)},
+             "ROW x RSC GEMM 512x2048x8192 (one core: its first 64 rows)")
+        also["c3"]["gpu_output_matches"] = _same(f3(), o3)
+    if "c4" in samples:
+        x4, wts, y4, sh = samples["c4"]
+        f4 = lambda: OCH.layer(x4, wts, "int4", sh.q_dim, sh.F, mm=OC.mm)[0]    # noqa: E731
+        lb = sh.layer_bytes("int4")
+        both("c4", f4, f4, lambda dt, one: {"us_per_layer": round(dt * 1e6, 1), "GBps": round(lb / dt / 1e9, 3)},
+             "one Qwen3-0.6B-shaped layer of int4x linears (QACT + MM each, 12 down chunks with ACC)")
+        also["c4"]["gpu_output_matches"] = _same(f4(), y4)
+    if "c5" in samples:
+        q5, S5, d5, r5, s5, l5, t5 = samples["c5"]
+        f5 = lambda: OC.mm(q5, S5, d5, r5, s5, "int8", 2560, flags=MM.RSC)   # noqa: E731
+        both("c5", f5, f5, lambda dt, one: {"GBps": round(c5_bytes() / dt / 1e9, 3)},
+             "LM head 262144x2560 RSC logits (greedy token checked separately)")
+        lg = f5()
+        also["c5"]["gpu_output_matches"] = _same(lg[0], l5) and OC.argmax(lg[0])[0] == t5
     return {"value": round(c2_bytes() / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"c2 int4 GEMV 6144x2048 (problem 0 of the timed launch), {reps} calls of the C oracle "
                       f"(oracle/cpu_mm.c, OpenMP), {dt * 1e3:.2f} ms per call",
-            "cpu_model": cpu_model(), "gpu_output_matches": matches,
-            "also": {"c_1_thread_GBps": round(c2_bytes() / dt1 / 1e9, 3), "c_1_thread_ms": round(dt1 * 1e3, 2),
-                     "numpy_oracle_GBps": round(c2_bytes() / dtn / 1e9, 3), "numpy_oracle_ms": round(dtn * 1e3, 1),
-                     "host_cores": os.cpu_count()}}
+            "cpu_model": cpu_model(), "gpu_output_matches": matches, "also": also}
 
 
 def main():
@@ -370,8 +439,8 @@ def main():
         ms2s = single_gemv_ms("int4", single2, N2, K2, 200)
         extra["c2_single_launch"] = {"us": round(ms2s * 1e3, 3),
                                      "GBps": round(c2_bytes() / (ms2s * 1e-3) / 1e9, 1)}
-    sample2 = tuple(t.cpu() for t in sample2)
-    del single2, rows2, srows2, q2, Sa2, da2, out2
+    samples = {"c2": tuple(t.cpu().numpy() for t in sample2)}
+    del single2, rows2, srows2, q2, Sa2, da2, out2, sample2
     torch.cuda.empty_cache()
 
     if "copy" in only:
@@ -384,11 +453,13 @@ def main():
                                      "GBps": round(B1 * c1_bytes() / (ms1 * 1e-3) / 1e9, 1)}
         ms1s = single_gemv_ms("int8", s1, 4096, 1024, 200, rsc=True)
         extra["c1_single_launch"] = {"us": round(ms1s * 1e3, 3)}
-        del s1
+        r1, sr1, q1, S1, d1, o1 = s1
+        samples["c1"] = tuple(t.cpu().numpy() for t in (r1[0], sr1[0], q1[:1], S1[:1], d1[:1], o1[:1]))
+        del s1, r1, sr1, q1, S1, d1, o1
         torch.cuda.empty_cache()
         print(f"[c1] {extra['c1_int8_rsc_gemv']}", file=sys.stderr, flush=True)
     if "c5" in only:
-        ms5, tok, ms_pick, ms_both = lm_head(10, 2)
+        ms5, tok, ms_pick, ms_both, samples["c5"] = lm_head(10, 2)
         extra["c5_lm_head_argmax"] = {"us": round(ms5 * 1e3, 2), "token": tok,
                                       "GBps": round(c5_bytes() / (ms5 * 1e-3) / 1e9, 1),
                                       "frac_hbm": round(c5_bytes() / (ms5 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -402,8 +473,10 @@ def main():
         # the same step as one launch per linear (the path the persistent step replaces)
         extra["c4_decode_step_launches"] = c4_step(10, 2, persistent=False)
         print(f"[c4 launches] {extra['c4_decode_step_launches']}", file=sys.stderr, flush=True)
+        if not args.no_cpu:
+            samples["c4"] = c4_layer_sample()
     if "c3" in only or "c3r" in only:
-        ms3 = gemm(20, 2)
+        ms3, samples["c3"] = gemm(20, 2)
         tops = 2 * 512 * 2048 * 8192 / (ms3 * 1e-3) / 1e12
         extra["c3_gemm_row_x_rsc"] = {"us": round(ms3 * 1e3, 2), "TOPS": round(tops, 2),
                                       "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
@@ -414,13 +487,15 @@ def main():
         del o3
         extra["c3_output_write_alone"] = {"us": round(msf * 1e3, 2), "what": "torch fill_ of the 512 x 8192 fp32 output"}
     if "c3" in only or "c3m" in only:
-        ms3m = gemm(20, 2, row_mode=False)
+        ms3m, _ = gemm(20, 2, row_mode=False)
         tops = 2 * 512 * 2048 * 8192 / (ms3m * 1e-3) / 1e12
         extra["c3_gemm_mx_x_rsc"] = {"us": round(ms3m * 1e3, 2), "TOPS": round(tops, 2),
                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         print(f"[c3 mx] {extra['c3_gemm_mx_x_rsc']}", file=sys.stderr, flush=True)
 
-    cpu = None if args.no_cpu else cpu_baseline(sample2)
+    cpu = None if args.no_cpu else cpu_baseline(samples)
+    if cpu is not None:
+        print(f"[cpu] {json.dumps(cpu['also'])}", file=sys.stderr, flush=True)
     line = {
         "metric": "quant GEMV GB/s (% HBM peak) + prefill int8 GEMM TOPS, 1 MI355X",
         "value": round(gbs2, 2),

@@ -93,6 +93,9 @@ def test_layer_small():
     assert same_bits(mid["h"], F.mul(mid["gu"][:, :Fd], mid["gu"][:, Fd:]))
     assert same_bits(y, CH.ranges_dot(mid["h"], wts["down"], "int4", 256))
     assert np.any(y != 0)
+    from oracle import cpu                  # the C MM in the same chain: the same bits
+    yc, midc = CH.layer(x, wts, "int4", qd, Fd, mm=cpu.mm)
+    assert all(same_bits(midc[k], mid[k]) for k in mid) and same_bits(yc, y)
 
 
 EMU_TOL = 1e-5       # of the largest output of each linear: the machine's fp32 chain vs float64
