@@ -108,22 +108,24 @@ static int check_mm(const char* who, const int8_t* q, int64_t ldq, const uint8_t
         return otpu_fail(OTPU_EALIGN, "%s: weight rows and activations 16-byte aligned (w, rs, q, ldq)", who);
     if (rs >= (1 << 24) || srs >= (1 << 24))
         return otpu_fail(OTPU_EINVAL, "%s: row strides of 16 MiB or more", who);
-    if ((rowb / 16 + 63) / 64 > LMAX)
-        return otpu_fail(OTPU_EINVAL, "%s: K %d exceeds the register-resident operand (%d 16-byte pieces a lane)",
-                         who, K, LMAX);
+    if (K > KMAX_MM) return otpu_fail(OTPU_EINVAL, "%s: K %d (at most %d: fewer than 256 blocks)", who, K, KMAX_MM);
     return OTPU_OK;
 }
 
-// lanes per row: the team size in {64, 32, 16} that wastes the fewest lane pieces
-static void pick_team(int P, int* T, int* L) {
+// lanes per row: the team size in {64, 32, 16} that wastes the fewest lane pieces; a row of
+// more than 64 LMAX pieces takes teams of 64 with LMAX pieces a lane, walked in segments
+static void pick_team(int P, int* T, int* L, int* nseg = nullptr) {
     int bt = 64, bl = (P + 63) / 64, bw = bl * 64 - P;
     for (int t = 32; t >= 16; t >>= 1) {
         int l = (P + t - 1) / t, w = l * t - P;
         if (l <= LMAX && w < bw) { bt = t; bl = l; bw = w; }
     }
     if (bl == 7) bl = 8;                        // (no L = 7 instantiation: the eighth is masked)
+    const int ns = bl > LMAX ? (bl + LMAX - 1) / LMAX : 1;
+    if (bl > LMAX) bl = LMAX;
     *T = bt;
     *L = bl;
+    if (nseg) *nseg = ns;
 }
 
 static int mr_max(int fmt, int L) {
@@ -134,7 +136,7 @@ static int launch_gemv(MMArgs a, int fmt, int batch, hipStream_t s) {
     const int64_t rowb = fmt == OTPU_INT8 ? a.K : a.K / 2;
     a.P = (int)(rowb / 16);
     int L = 1;
-    pick_team(a.P, &a.T, &L);
+    pick_team(a.P, &a.T, &L, &a.nseg);
     const int M = a.M, cap = mr_max(fmt, L);
     for (int j0 = 0; j0 < M; j0 += cap) {        // activation rows in chunks the registers hold
         MMArgs c = a;
@@ -273,9 +275,9 @@ int qin_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float
              int nsum, int64_t sum_stride, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
              int64_t srs, int N, int fmt, int flags, int k0, float* out, int64_t ors, int64_t part_stride) {
     const int chunk = fmt == OTPU_INT8 ? OTPU_D : 2 * OTPU_D;
-    if (width < chunk || width % chunk || K % width || width > QIN_KMAX)
+    if (width < chunk || width % chunk || K % width || width > QIN_KBIG)
         return otpu_fail(OTPU_EINVAL, "mm_qin: ranges of %d over K %d (multiples of %d, at most %d)", width, K, chunk,
-                         QIN_KMAX);
+                         QIN_KBIG);
     if (flags & (OTPU_ACC | OTPU_ASCALE | OTPU_RMAX)) return otpu_fail(OTPU_EINVAL, "mm_qin: no ACC, ASCALE or RMAX");
     if (!x || !out || nsum < 1 || nsum > QIN_NSUM_MAX || (nsum > 1 && sum_stride < K) || ors < N)
         return otpu_fail(OTPU_EINVAL, "mm_qin: x / out NULL, nsum %d, sum_stride %lld, ors %lld", nsum,
@@ -297,7 +299,7 @@ int qin_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float
     a.rscale = rscale; a.cscale = cscale;
     a.w_bs = fmt == OTPU_INT8 ? width : width / 2; a.k0_bs = plain ? 0 : width / OTPU_D;
     a.P = (fmt == OTPU_INT8 ? width : width / 2) / 16;
-    pick_team(a.P, &a.T, Lp);
+    pick_team(a.P, &a.T, Lp, &a.nseg);
     *ap = a;
     return OTPU_OK;
 }

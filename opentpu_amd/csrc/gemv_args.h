@@ -12,7 +12,8 @@ namespace otpu {
 constexpr int GEMV_THREADS = 256;
 constexpr int LM_WORDS = 64;      // the LM head's running maxima (one line each)
 constexpr int LM_STRIDE = 32;     // u64 words from one to the next (256 bytes)
-constexpr int LMAX = 8;            // pieces per lane held in registers (K <= 128 * LMAX * 16 / elements)
+constexpr int LMAX = 8;            // pieces per lane held in registers at once (a segment of a row)
+constexpr int KMAX_MM = 32640;     // K an MM takes: blocks of 128 below 256 (isa.py's 8-bit KB field)
 
 struct MMArgs {
     const int8_t* q; int64_t ldq;
@@ -30,6 +31,7 @@ struct MMArgs {
                                    // LM_STRIDE apart (workgroup b raises word b % LM_WORDS)
     int64_t base;                  // LM head: index of row 0
     int P, T;                      // 16-byte pieces per row, lanes per row (team)
+    int nseg;                      // segments a row is walked in: T * L pieces each (0 or 1: one)
     // batch strides (elements of each pointer's type; bytes for w / ws; blocks for k0)
     int64_t q_bs, sa_bs, da_bs, w_bs, ws_bs, out_bs;
     int k0_bs;
@@ -68,7 +70,8 @@ struct MMArgs {
     } while (0)
 #endif
 
-constexpr int QIN_KMAX = 4096;     // columns a prologue QACT holds in LDS
+constexpr int QIN_KMAX = 4096;     // columns the persistent chain's and the fold's prologue QACT hold in LDS
+constexpr int QIN_KBIG = 16384;    // columns otpu_mm_qin's prologue QACT holds in LDS (its widest kernels)
 constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds
 
 // rows a team takes per iteration: 8 rows' loads in flight per wave for one activation row

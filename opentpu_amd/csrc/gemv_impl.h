@@ -243,12 +243,53 @@ __device__ __forceinline__ void ll_drain(const MMArgs& a, int from, int to) {
     }
 }
 
-// the prologue QACT's LDS: the quantized row, its group offsets, the waves' maxima
-struct QinLds {
-    uint32_t qs[QIN_KMAX / 4];
-    uint8_t ds[QIN_KMAX / 32];
+// the prologue QACT's LDS: the quantized row, its group offsets, the waves' maxima (KM columns)
+template <int KM>
+struct QinLdsT {
+    uint32_t qs[KM / 4];
+    uint8_t ds[KM / 32];
     uint32_t red[4];
 };
+using QinLds = QinLdsT<QIN_KMAX>;
+
+// the columns a QACT prologue of L pieces a lane and teams of T holds: one walk of the row, or
+// (L = LMAX, a kernel of its own, not the chain's) rows up to QIN_KBIG walked in segments
+template <int FMT, int L, int T, bool LL>
+constexpr int qin_cols() {
+    constexpr int one = L * T * (FMT == OTPU_INT8 ? 16 : 32);
+    return LL ? QIN_KMAX : (L == LMAX ? QIN_KBIG : (one < QIN_KBIG ? one : QIN_KBIG));
+}
+
+// the activation pieces pbase + i T + tl (i < L) of lane tl from the quantized row in LDS, and
+// their W - da (a piece past P gets a negative shift: its terms drop); 4-bit layouts split even
+// / odd elements, as the loaded path permutes them
+template <int FMT, int L, int T>
+__device__ __forceinline__ void qin_act(const uint32_t* qs, const uint8_t* ds, int P, int pbase, int tl, int W,
+                                        uint32_t (&act)[L][FMT == OTPU_INT8 ? 4 : 8], int (&shA)[L]) {
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+        const int p = pbase + i * T + tl;
+        const bool ok = p < P;
+        if (FMT == OTPU_INT8) {
+            const uint4 q4 = ok ? reinterpret_cast<const uint4*>(qs)[p] : make_uint4(0, 0, 0, 0);
+            act[i][0] = q4.x; act[i][1] = q4.y; act[i][2] = q4.z; act[i][3] = q4.w;
+            shA[i] = W - (ok ? (int)ds[p >> 1] : 0);
+        } else {
+            uint4 v0 = make_uint4(0, 0, 0, 0), v1 = v0;
+            if (ok) {
+                v0 = reinterpret_cast<const uint4*>(qs)[2 * p];
+                v1 = reinterpret_cast<const uint4*>(qs)[2 * p + 1];
+            }
+            const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                act[i][2 * t] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x06040200u);
+                act[i][2 * t + 1] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x07050301u);
+            }
+            shA[i] = W - (ok ? (int)ds[p] : 0);
+        }
+    }
+}
 
 // QACT of the problem's fp32 row in the prologue (fp32.quantize_mx(x, 32) of one row, as
 // qact_kernel computes it), once per workgroup: each thread takes float4 chunks of the row
@@ -266,26 +307,37 @@ struct QinLds {
 // phases); LLIN: the row comes from the hand-off entries a.ll_in (the weights and scale factors
 // go out first: they do not wait for the hand-off), else from the plain row (the step's first
 // phase).
+// qs_out / ds_out (optional): where the quantized row and its offsets stay in LDS (the rows of
+// more than one walk read their later segments' pieces from there, qin_act)
 template <int FMT, int L, int T, bool LL = false, bool LLIN = LL, int NRM = 0, typename IssueWeights>
 __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&act)[L][FMT == OTPU_INT8 ? 4 : 8],
                                              int (&shA)[L], float& sa2, IssueWeights&& issue_weights,
-                                             QinLds* lds = nullptr) {
-    QinLds* S;
+                                             QinLds* lds = nullptr, const uint32_t** qs_out = nullptr,
+                                             const uint8_t** ds_out = nullptr) {
+    constexpr int KM = qin_cols<FMT, L, T, LL>();
+    uint32_t* qs;
+    uint8_t* ds;
+    uint32_t* red;
     if constexpr (LL) {
-        S = lds;
+        qs = lds->qs;
+        ds = lds->ds;
+        red = lds->red;
     } else {
-        __shared__ __align__(16) QinLds own;
-        S = &own;
+        __shared__ __align__(16) QinLdsT<KM> own;
+        qs = own.qs;
+        ds = own.ds;
+        red = own.red;
     }
-    uint32_t* qs = S->qs;
-    uint8_t* ds = S->ds;
-    uint32_t* red = S->red;
-    // float4 chunks a thread holds at most: the row has at most L T pieces of 16 (int8) or 32
-    // (4-bit) elements, so for the small rows of a chain only the chunks that can exist are
-    // compiled (the code runs once per launch, from a cold instruction cache)
+    if (qs_out) *qs_out = qs;
+    if (ds_out) *ds_out = ds;
+    // float4 chunks a thread holds at most: the row has at most KM elements (L T pieces of 16
+    // (int8) or 32 (4-bit) elements in one walk), so for the small rows of a chain only the
+    // chunks that can exist are compiled (the code runs once per launch, from a cold
+    // instruction cache)
     constexpr int EPP = FMT == OTPU_INT8 ? 16 : 32;
     constexpr int CPT0 = (L * T * EPP / 4 + 255) / 256;
-    constexpr int CPT = CPT0 < QIN_KMAX / 4 / 256 ? CPT0 : QIN_KMAX / 4 / 256;
+    constexpr int KC = (KM / 4 + 255) / 256;              // chunks a thread of the LDS's KM columns
+    constexpr int CPT = (L == LMAX && !LL) || CPT0 > KC ? KC : CPT0;
     const int K = a.K, NC = K >> 2, W = window_of(FMT);
     // (workgroups of 256 threads: the mask tells the compiler so, and the chunk tests below then
     // resolve at compile time where K is a constant)
@@ -431,30 +483,7 @@ __device__ __forceinline__ void qin_prologue(const MMArgs& a, int b, uint32_t (&
         }
     }
     __syncthreads();
-    const int tl = tid & (T - 1);
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-        const int p = i * T + tl;
-        const bool ok = p < a.P;
-        if (FMT == OTPU_INT8) {
-            const uint4 q4 = ok ? reinterpret_cast<const uint4*>(qs)[p] : make_uint4(0, 0, 0, 0);
-            act[i][0] = q4.x; act[i][1] = q4.y; act[i][2] = q4.z; act[i][3] = q4.w;
-            shA[i] = W - (ok ? (int)ds[p >> 1] : 0);
-        } else {
-            uint4 v0 = make_uint4(0, 0, 0, 0), v1 = v0;
-            if (ok) {
-                v0 = reinterpret_cast<const uint4*>(qs)[2 * p];
-                v1 = reinterpret_cast<const uint4*>(qs)[2 * p + 1];
-            }
-            const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                act[i][2 * t] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x06040200u);
-                act[i][2 * t + 1] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x07050301u);
-            }
-            shA[i] = W - (ok ? (int)ds[p] : 0);
-        }
-    }
+    qin_act<FMT, L, T>(qs, ds, a.P, 0, tid & (T - 1), W, act, shA);
 }
 
 // the kernel body for a team of T lanes (T a compile-time constant: the exchanges of the
@@ -464,6 +493,7 @@ template <int FMT, int MR, int L, int T, bool PLAIN, bool QIN, int R, bool LL = 
 __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr) {
     constexpr int AW = FMT == OTPU_INT8 ? 4 : 8;          // activation dwords per piece
     constexpr int E = R * MR;                             // sums a lane carries per iteration
+    constexpr bool SEGS = L == LMAX && !QIN && !LL;       // rows of more pieces than one walk holds
     static_assert(E <= T, "a team holds its E sums after the reduce-scatter");
     const int lane = threadIdx.x & 63;
     constexpr int NT = 64 / T;                            // teams per wave
@@ -496,12 +526,12 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
     constexpr int AQ = FMT == OTPU_INT8 ? 1 : 2;          // 16-byte loads a piece
     uint4 araw[MR][L][AQ];
     int draw[MR][L];
-    auto act_issue = [&] {
+    auto act_issue = [&](int pbase) {
 #pragma unroll
         for (int j = 0; j < MR; ++j) {
 #pragma unroll
             for (int i = 0; i < L; ++i) {
-                const int p = i * T + tl;
+                const int p = pbase + i * T + tl;
                 const bool ok = p < P && j < a.M;
                 const int8_t* qp = q + (ok ? j * a.ldq + 16 * AQ * p : 0);
 #pragma unroll
@@ -510,7 +540,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             }
         }
     };
-    auto act_finish = [&] {
+    auto act_finish = [&](int pbase) {
 #pragma unroll
         for (int j = 0; j < MR; ++j) {
 #pragma unroll
@@ -527,7 +557,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
                         act[j][i][2 * t + 1] = __builtin_amdgcn_perm(d[2 * t + 1], d[2 * t], 0x07050301u);
                     }
                 }
-                const bool ok = i * T + tl < P && j < a.M;
+                const bool ok = pbase + i * T + tl < P && j < a.M;
                 shA[j][i] = ok ? W - draw[j][i] : -4096;
             }
         }
@@ -565,7 +595,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
     constexpr bool PAIRS = LL && R == 4 && NT == 2;
     const int gp = PAIRS ? a.gu_pair : 0;
     auto slot_row = [&](int r) { return (r >= 2 ? gp : 0) + 2 * team + (r & 1); };
-    auto load = [&](Stage& st, int n0) {
+    auto load = [&](Stage& st, int n0, int pbase = 0) {
         const int base = gp ? n0 / 2 : n0;
         const uint8_t* wb = w + (int64_t)base * a.rs;
         const uint8_t* sb = ws + (int64_t)base * a.srs;
@@ -577,7 +607,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             const uint32_t soff = (uint32_t)dn * (uint32_t)a.srs;
 #pragma unroll
             for (int i = 0; i < L; ++i) {
-                const int p = i * T + tl;
+                const int p = pbase + i * T + tl;
                 const int pc = p < P ? p : P - 1;
                 st.wv[r][i] = ld16(wb + (roff + 16u * (uint32_t)pc));
                 st.sc[r][i] = piece_scale<FMT>(sb, soff, k0, pc, plain);
@@ -589,8 +619,8 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         const float swr = unit ? 1.0f : *reinterpret_cast<const float*>(sb + (uint32_t)de * (uint32_t)a.srs);
         st.sw = LL ? swr : ftz(swr);
     };
-    auto compute = [&](const Stage& st, int n0) {
-        double v[E];
+    // the exact sums of one segment's pieces (pbase on): v = them (first), else v += them
+    auto dots = [&](const Stage& st, double (&v)[E], int pbase, bool first) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
 #pragma unroll
@@ -600,11 +630,13 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
                 for (int i = 0; i < L; ++i) {
                     int c0, c1;
                     piece_dot<FMT>(st.wv[r][i], act[j][i], c0, c1);
-                    acc += piece_term<FMT, PLAIN>(c0, c1, st.sc[r][i], shA[j][i], i * T + tl);
+                    acc += piece_term<FMT, PLAIN>(c0, c1, st.sc[r][i], shA[j][i], pbase + i * T + tl);
                 }
-                v[r * MR + j] = acc;
+                v[r * MR + j] = first ? acc : v[r * MR + j] + acc;
             }
         }
+    };
+    auto epilogue = [&](double (&v)[E], float sw, int n0) {
         // reduce-scatter over the team: each step halves the values a lane carries (E - 1
         // exchanges in all: permlane swaps across lane bits 5 and 4, DPP below), then plain
         // steps finish the sums over the team's T lanes
@@ -620,7 +652,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
         if constexpr (LL) {                           // (QIN, one activation row, no flags)
             // every lane forms its y (only the epilogue lanes' are kept): the pairs' exchange
             // below needs the whole wave
-            const float y = fmul_f(fmul_f((float)tot, ftz(st.sw)), sa2[0]);
+            const float y = fmul_f(fmul_f((float)tot, ftz(sw)), sa2[0]);
             if (gp) {
                 const float yu = __uint_as_float(
                     __builtin_amdgcn_permlane16_swap(fbits(y), fbits(y), false, false)[1]);
@@ -645,7 +677,7 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             } else {
                 // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw
                 // and the finished Sa * 2^-W need no operand flush
-                float y = fmul_f(fmul_f((float)tot, st.sw), sa2[ej]);
+                float y = fmul_f(fmul_f((float)tot, sw), sa2[ej]);
                 if constexpr (QIN) {                  // (no ACC / ASCALE / RMAX / LM head here)
                     out[(int64_t)ej * a.ors + n] = y;
                     return;
@@ -664,11 +696,46 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             }
         }
     };
+    auto compute = [&](const Stage& st, int n0) {
+        double v[E];
+        dots(st, v, 0, true);
+        epilogue(v, st.sw, n0);
+    };
 
     // one stage per wave: the loads of an iteration go out together and the waves of the SIMD
     // (5-8 resident) overlap each other's memory latency; a second register stage per wave
     // costs occupancy and measured slower on MI355X
-    if constexpr (QIN) {
+    if constexpr (QIN && L == LMAX && !LL) {
+        // (the widest prologue: rows of more than one walk read each segment's pieces from LDS)
+        Stage st;
+        const int nfirst = wave * RW;
+        const uint32_t* qs = nullptr;
+        const uint8_t* ds = nullptr;
+        qin_prologue<FMT, L, T, LL, LLIN, NRM>(a, b, act[0], shA[0], sa2[0], [&] {
+            if (nfirst < a.N) load(st, nfirst);
+        }, lds, &qs, &ds);
+        if (a.nseg > 1) {
+            const int PS = T * L;
+            for (int n0 = nfirst; n0 < a.N; n0 += stride) {
+                double v[E];
+                float sw = 0.0f;
+                for (int sg = 0; sg < a.nseg; ++sg) {
+                    if (sg > 0 || n0 != nfirst) {
+                        qin_act<FMT, L, T>(qs, ds, P, sg * PS, tl, W, act[0], shA[0]);
+                        load(st, n0, sg * PS);
+                    }
+                    dots(st, v, sg * PS, sg == 0);
+                    sw = st.sw;
+                }
+                epilogue(v, sw, n0);
+            }
+        } else {
+            for (int n0 = nfirst; n0 < a.N; n0 += stride) {
+                if (n0 != nfirst) load(st, n0);
+                compute(st, n0);
+            }
+        }
+    } else if constexpr (QIN) {
         // the first rows stream in while the workgroup quantizes the activation row
         Stage st;
         const int nfirst = wave * RW;
@@ -680,14 +747,32 @@ __device__ __forceinline__ void gemv_body(const MMArgs& a, QinLds* lds = nullptr
             if (n0 != nfirst) load(st, n0);
             compute(st, n0);
         }
+    } else if (SEGS && a.nseg > 1) {
+        // a row longer than the registers hold (T L pieces): each row group is walked in nseg
+        // segments, the activation pieces of a segment loaded again for it (from the caches:
+        // the row is small and every wave reads it), the exact double sums carried across
+        const int PS = T * L;
+        for (int n0 = wave * RW; n0 < a.N; n0 += stride) {
+            double v[E];
+            float sw = 0.0f;
+            for (int sg = 0; sg < a.nseg; ++sg) {
+                Stage st;
+                act_issue(sg * PS);
+                load(st, n0, sg * PS);
+                act_finish(sg * PS);
+                dots(st, v, sg * PS, sg == 0);
+                sw = st.sw;
+            }
+            epilogue(v, sw, n0);
+        }
     } else {
         // the first rows stream in while the activation row loads
-        act_issue();
+        act_issue(0);
         const int nfirst = wave * RW;
         if (nfirst < a.N) {
             Stage st;
             load(st, nfirst);
-            act_finish();
+            act_finish(0);
             compute(st, nfirst);
         }
         for (int n0 = nfirst + stride; n0 < a.N; n0 += stride) {
