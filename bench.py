@@ -171,9 +171,10 @@ def lm_head(steps, warmup):
     return ms, int(tok.item()), ms_pick, ms_both, sample
 
 
-def gemm(steps, warmup, row_mode=True):
-    """The c3 prefill GEMM, RSC weights; activations ROW-quantized (the headline: one scale a
-    row, a single exact plane) or MX (group offsets: several planes)."""
+def gemm(steps, warmup, row_mode=True, fmt="int8"):
+    """The c3 prefill GEMM, RSC weights (fmt int8) or 4-bit group-quantized ones (int4x / fp4x6:
+    the 4-bit GEMM); activations ROW-quantized (the headline: one scale a row, a single exact
+    plane) or MX (group offsets: several planes)."""
     import torch
 
     from opentpu_amd import _lib as X
@@ -181,14 +182,15 @@ def gemm(steps, warmup, row_mode=True):
     M, K, N = 512, 2048, 8192
     gen = torch.Generator(device="cuda").manual_seed(3)
     W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
-    rows, srows = quant.quantize_mxu(W, "int8", rsc=True)
+    rows, srows = quant.quantize_mxu(W, "int8", rsc=True) if fmt == "int8" else quant.quantize_mxu(W, fmt)
+    fl = X.RSC if fmt == "int8" else 0
     x = torch.randn((M, K), generator=gen, device="cuda")
     q, Sa, da = fp32.quantize_mx(x, 32, row_mode=row_mode)
     out = torch.empty((M, N), dtype=torch.float32, device="cuda")
 
     def step():
-        X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, M, K, X.ptr(rows), K, X.ptr(srows), 4, N,
-               X.FMT["int8"], X.RSC, 0, None, X.ptr(out), N, None, X.stream())
+        X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, M, K, X.ptr(rows), rows.shape[1], X.ptr(srows),
+               srows.shape[1], N, X.FMT[fmt], fl, 0, None, X.ptr(out), N, None, X.stream())
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
     sample = tuple(t.cpu().numpy() for t in (q, Sa, da, rows, srows, out))
     return ms, sample
@@ -410,8 +412,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=80)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c3r,c3m,c4,c5,copy (default: c1,c2s,c3,c4,c5; "
-                    "c3r / c3m: the ROW / the MX GEMM alone); "
+    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c3r,c3m,c3q,c4,c5,copy (default: c1,c2s,c3,c4,"
+                    "c5; c3r / c3m: the ROW / the MX int8 GEMM alone; c3q: the 4-bit GEMMs alone); "
                     "the headline c2 always runs, c2s adds its single-launch figure")
     ap.add_argument("--summarize", metavar="DIR", help="print a text summary of rocprofv3 CSV output and exit")
     args = ap.parse_args()
@@ -492,6 +494,16 @@ def main():
         extra["c3_gemm_mx_x_rsc"] = {"us": round(ms3m * 1e3, 2), "TOPS": round(tops, 2),
                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         print(f"[c3 mx] {extra['c3_gemm_mx_x_rsc']}", file=sys.stderr, flush=True)
+    if "c3" in only or "c3q" in only:
+        # the c3 shape with 4-bit group-quantized weights (int4x, fp4x6): the 4-bit GEMM, whose
+        # two weight planes make two int8 MFMA products of the c3 size
+        for f4 in ("int4", "fp4"):
+            for rm, tag in ((True, "row"), (False, "mx")):
+                ms4, _ = gemm(20, 2, row_mode=rm, fmt=f4)
+                tops = 2 * 512 * 2048 * 8192 / (ms4 * 1e-3) / 1e12
+                extra[f"c3_gemm_{tag}_x_{f4}x"] = {"us": round(ms4 * 1e3, 2), "TOPS": round(tops, 2),
+                                                   "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+                print(f"[c3 {f4} {tag}] {extra[f'c3_gemm_{tag}_x_{f4}x']}", file=sys.stderr, flush=True)
 
     cpu = None if args.no_cpu else cpu_baseline(samples)
     if cpu is not None:

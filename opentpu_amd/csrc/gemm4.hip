@@ -1,0 +1,560 @@
+// MM for many activation rows with 4-bit weights (int4x, fp4x6, and their RSC / UNIT forms) on
+// the int8 MFMA units: the prefill GEMM of the 4-bit formats.  Semantics: opentpu/isasim.py:
+// 749-910 (docs/isa.md:226-305): acc = sum over 32-groups of [sh >= 0] m 2^sh c, sh = 11 - dw -
+// da, c the group's integer dot product; y = (i2f(acc) * Sw) * (Sa * 2^-11).
+//
+// Exactness.  Every product term is folded into an integer weight before the MFMA.  For weight
+// row n let R_n be the largest block offset dw <= 11 (a block with dw > 11 drops for every
+// activation offset).  For the activation plane d (the 32-groups whose offset is d):
+//     acc_d = 2^(11 - R_n - d) * sum_i q_i w''_i,   w''_i = [dw + d <= 11] m 2^(R_n - dw) w_i,
+// an ordinary integer matrix product of int8 activations and the integer w'' (|w''| < 2^15 when
+// the tile's offsets and multipliers allow: checked per tile).  w'' is split into two int8 planes
+// in balanced base 256 (w'' = 256 h + l, l and h in [-128, 127]), each an int8 MFMA operand, so
+// the K walk is a plain two-plane int8 GEMM with no rescaling inside it.  Activation planes (MX
+// offsets) walk K once each, combined by Horner's rule in the int32 accumulators (acc <<= the gap
+// to the next plane's d, as the int8 GEMM does; the bound is checked per tile).  The epilogue
+// forms T = 256 C_h + C_l in int64 and shifts it by 11 - R_n - d_last (exact: the accumulator is
+// an integer), then the reference's fp32 epilogue.  A tile the bounds refuse takes an exact VALU
+// path.
+//
+// Work layout.  A workgroup of 8 waves owns a 128 x 128 output tile.  Waves 0-3 multiply (64 x 64
+// each, 4 x 4 v_mfma_i32_16x16x64_i8 per 64-deep step and plane); waves 4-7 stream and expand:
+// they issue every direct-to-LDS load (the activation stage, a 3-deep ring; the 4-bit rows of a
+// stage with their scale words and the activation offset words, a 4-deep ring one stage further
+// ahead) and turn the nibbles of the next stage into the two int8 planes (a 16-entry table per
+// 32-group and plane, built with packed 16-bit products and read with v_perm_b32), while the
+// multiplying waves run the current stage's MFMAs.  One workgroup barrier a stage.
+#include "otpu_common.h"
+
+namespace otpu {
+namespace g4 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int TM = 128, TN = 128, BK = 128;      // tile rows and columns, K a stage (one block)
+constexpr int W4 = 11;                          // the 4-bit formats' window
+constexpr int NA = 3;                           // activation stages in their ring
+constexpr int NR = 4;                           // raw weight stages in theirs
+constexpr int ATILE = TM * BK;                  // 16 KB of activations a stage
+constexpr int RAWB = TN * BK / 2;               // 8 KB of nibbles a stage
+constexpr int RSLOT = RAWB + 512 + 512;         // nibbles, scale words, activation offset words
+constexpr int PLANE = TN * BK;                  // one int8 plane of a stage's weights: 16 KB
+constexpr int OFF_RAW = NA * ATILE;
+constexpr int OFF_PL = OFF_RAW + NR * RSLOT;
+constexpr int LDS_BYTES = OFF_PL + 2 * 2 * PLANE;
+constexpr int TPS = 68;                         // the epilogue's transpose row stride (words)
+static_assert(4 * 2 * 64 * TPS * 4 <= LDS_BYTES, "the epilogue's two planes a wave fit the walk's memory");
+static_assert(LDS_BYTES <= 160 * 1024, "one workgroup a CU");
+
+struct Args {
+    const int8_t* q; int64_t ldq;
+    const float* Sa;
+    const uint8_t* da; int64_t ldda;
+    int M, K;
+    const uint8_t* w; int64_t rs;
+    const uint8_t* ws; int64_t srs;
+    int N, flags, k0;
+    const float* alpha;
+    float* out; int64_t ors;
+    int tiles_m, tiles_n;
+    int vec4;
+};
+
+// the 16-byte slot of chunk c of row r (128-byte rows): the XOR swizzle that puts the 16 rows a
+// ds_read_b128 fragment reads on distinct banks (the int8 GEMM's)
+__device__ __forceinline__ int rswz(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+__device__ __forceinline__ int rof(int r, int c) { return r * BK + ((c ^ rswz(r)) << 4); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// direct-to-LDS loads: 16 bytes (lane L at M0 + 16 L) and 4 bytes (lane L at M0 + 4 L) a lane
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+// LDS reads and writes of this wave done, then the workgroup barrier
+__device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
+
+// direct loads a streaming wave issues: per activation stage (16 KB over 4 waves) and per raw
+// stage (8 KB of nibbles over 4 waves, then one dword a lane: scale words or offset words)
+constexpr int DMA_A = 4, DMA_R = 3;
+
+// ---- the value tables of one 32-group: codes 0..15 times its integer multiplier ----
+// pair k of a format: the values of codes 2k and 2k + 1 (int4 two's complement; fp4x6 twice the
+// E2M1 value, sign in bit 3), as two 16-bit lanes
+template <int FMT>
+__device__ __forceinline__ uint32_t code_pair(int k) {
+    constexpr int mag[8] = {0, 1, 2, 3, 4, 6, 8, 12};
+    int v0, v1;
+    if (FMT == OTPU_INT4) {
+        v0 = 2 * k < 8 ? 2 * k : 2 * k - 16;
+        v1 = 2 * k + 1 < 8 ? 2 * k + 1 : 2 * k + 1 - 16;
+    } else {
+        v0 = (2 * k) & 8 ? -mag[(2 * k) & 7] : mag[(2 * k) & 7];
+        v1 = (2 * k + 1) & 8 ? -mag[(2 * k + 1) & 7] : mag[(2 * k + 1) & 7];
+    }
+    return ((uint32_t)v0 & 0xFFFFu) | ((uint32_t)v1 << 16);
+}
+
+__device__ __forceinline__ uint32_t as_u32(s16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ s16x2 as_s16x2(uint32_t v) { return __builtin_bit_cast(s16x2, v); }
+
+// the l and h tables of multiplier mp (|code value * mp| <= 32256): tl[k] holds the low bytes of
+// codes 4k .. 4k + 3, th[k] their high bytes (v = 256 h + l, both signed bytes)
+template <int FMT>
+__device__ __forceinline__ void group_tables(int mp, uint32_t (&tl)[4], uint32_t (&th)[4]) {
+    const s16x2 mm = as_s16x2((uint32_t)mp * 0x00010001u);
+    uint32_t p[8], h[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const s16x2 v = mm * as_s16x2(code_pair<FMT>(k));            // v_pk_mul_lo_u16
+        p[k] = as_u32(v);
+        h[k] = as_u32(v + as_s16x2(0x00800080u));                    // v_pk_add_u16: (v + 128)
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        tl[k] = __builtin_amdgcn_perm(p[2 * k + 1], p[2 * k], 0x06040200u);   // low bytes: l
+        th[k] = __builtin_amdgcn_perm(h[2 * k + 1], h[2 * k], 0x07050301u);   // high bytes of v + 128: h
+    }
+}
+
+// the table entries of the four codes in the bytes of s (each 0..15)
+__device__ __forceinline__ uint32_t lookup(const uint32_t (&t)[4], uint32_t sel7, uint32_t pick) {
+    const uint32_t a = __builtin_amdgcn_perm(t[1], t[0], sel7);       // codes 0..7
+    const uint32_t b = __builtin_amdgcn_perm(t[3], t[2], sel7);       // codes 8..15
+    return __builtin_amdgcn_perm(b, a, pick);                         // byte i: a's or b's (bit 3)
+}
+
+// one raw dword (elements 0..7 of 8, element 2i in the low nibble of byte i) -> its l and h
+// bytes in element order (two dwords each)
+template <bool HI>
+__device__ __forceinline__ void expand8(uint32_t x, const uint32_t (&tl)[4], const uint32_t (&th)[4], uint32_t& l0,
+                                        uint32_t& l1, uint32_t& h0, uint32_t& h1) {
+    const uint32_t ev = x & 0x0F0F0F0Fu, od = (x >> 4) & 0x0F0F0F0Fu;   // elements 0 2 4 6, 1 3 5 7
+    const uint32_t se = ev & 0x07070707u, so = od & 0x07070707u;
+    const uint32_t pe = ((ev >> 1) & 0x04040404u) | 0x03020100u, po = ((od >> 1) & 0x04040404u) | 0x03020100u;
+    const uint32_t le = lookup(tl, se, pe), lo = lookup(tl, so, po);
+    l0 = __builtin_amdgcn_perm(lo, le, 0x05010400u);                  // elements 0 1 2 3
+    l1 = __builtin_amdgcn_perm(lo, le, 0x07030602u);                  // elements 4 5 6 7
+    if (HI) {
+        const uint32_t he = lookup(th, se, pe), ho = lookup(th, so, po);
+        h0 = __builtin_amdgcn_perm(ho, he, 0x05010400u);
+        h1 = __builtin_amdgcn_perm(ho, he, 0x07030602u);
+    }
+}
+
+// the exact MM integer of output (j, n), group by group (the tiles the planes' bounds refuse)
+template <int FMT>
+__device__ int64_t valu_acc4(const Args& a, int j, int n, bool plainw) {
+    constexpr int mag[8] = {0, 1, 2, 3, 4, 6, 8, 12};
+    const int8_t* qr = a.q + (int64_t)j * a.ldq;
+    const uint8_t* wr = a.w + (int64_t)n * a.rs;
+    const uint8_t* srow = a.ws + (int64_t)n * a.srs;
+    int64_t acc = 0;
+    for (int g = 0; g < a.K / 32; ++g) {
+        int c = 0;
+        for (int i = 0; i < 32; ++i) {
+            const int code = (wr[16 * g + i / 2] >> (4 * (i & 1))) & 15;
+            const int v = FMT == OTPU_INT4 ? (code < 8 ? code : code - 16) : (code & 8 ? -mag[code & 7] : mag[code & 7]);
+            c += (int)qr[32 * g + i] * v;
+        }
+        int dw = 0, m = 1;
+        if (!plainw) {
+            const uint32_t word = *reinterpret_cast<const uint32_t*>(srow + 8 + 4 * (a.k0 + g / 4));
+            dw = (int)(word & 0xFF);
+            m = (int)((word >> (8 + 6 * (g & 3))) & 63);
+        }
+        const int sh = W4 - dw - (int)a.da[(int64_t)j * a.ldda + g];
+        if (sh >= 0) acc += ((int64_t)m * c) << sh;
+    }
+    return acc;
+}
+
+// y = (i2f(acc) * Sw) * (Sa * 2^-11), then ACC / ASCALE (the reference's epilogue order)
+__device__ __forceinline__ void store_out(const Args& a, int m, int n, int64_t acc, float sw, float sa2) {
+    float y = fmul_f(fmul_f(i2f(acc), sw), sa2);
+    float* o = a.out + (int64_t)m * a.ors + n;
+    if (a.flags & OTPU_ASCALE) y = fadd(fmul(*o, a.alpha[m]), y);
+    else if (a.flags & OTPU_ACC) y = fadd(*o, y);
+    *o = y;
+}
+
+// HI: weights with scale rows (two int8 planes); false: RSC / UNIT weights (w'' = w, one plane)
+template <int FMT, bool HI>
+__global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
+    __shared__ __align__(16) int8_t lds[LDS_BYTES];
+    __shared__ int sR[TN];                      // each weight row's R (the largest live dw)
+    __shared__ float sSa2[TM];                  // the tile rows' Sa * 2^-11
+    __shared__ uint32_t sFlag[16];              // per wave: d values present, offsets past the window, PL
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool streamer = wid >= 4;
+    // XCD-major tile order (workgroup b runs on XCD b % 8): the tiles of one XCD share weight panels
+    int tm, tn;
+    {
+        const int b = blockIdx.x, ntiles = a.tiles_m * a.tiles_n;
+        if (ntiles % 8 == 0 && a.tiles_n % 8 == 0) {
+            const int t = (b % 8) * (ntiles / 8) + b / 8;
+            tn = t / a.tiles_m;
+            tm = t % a.tiles_m;
+        } else {
+            tn = b / a.tiles_m;
+            tm = b % a.tiles_m;
+        }
+    }
+    const int m0 = tm * TM, n0 = tn * TN;
+    const bool unit = (a.flags & OTPU_UNIT) != 0;
+    const bool plainw = unit || (a.flags & OTPU_RSC) != 0;
+    const int KS = a.K / BK;
+    constexpr int MAGMAX = FMT == OTPU_INT4 ? 8 : 12;
+
+    // ---- the tile's scan: activation offsets (waves 0-3), weight offsets and multipliers (4-7) ----
+    if (!streamer) {
+        if (tid < TM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-W4)) : 0.0f;
+        // two threads a row, a word of four offsets a load (ldda and da 4-byte aligned), the
+        // loads of 8 words in flight at once (one at a time, each waited on, the scan took ~30 us)
+        uint32_t dm = 0;
+        const int r = tid & (TM - 1), h = tid >> 7;
+        if (m0 + r < a.M) {
+            const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)(m0 + r) * a.ldda);
+#pragma unroll 8
+            for (int k = h; k < KS; k += 2) {
+                const uint32_t wd = drow[k];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t d = (wd >> (8 * t)) & 0xFFu;
+                    dm |= 1u << (d <= W4 ? d : 31);
+                }
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) dm |= __shfl_xor(dm, o, 64);
+        if (lane == 0) sFlag[wid] = dm;
+    } else {
+        const int ht = tid - 256, r = ht >> 1, h = ht & 1;
+        int R = 0, T = 0;
+        if (!plainw) {                          // (rows past N: the last row's, which they stream)
+            const uint8_t* srow = a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
+#pragma unroll 8
+            for (int k = h; k < KS; k += 2) {
+                const uint32_t word = *reinterpret_cast<const uint32_t*>(srow + 4 * k);
+                const int dw = (int)(word & 0xFF);
+                if (dw > W4) continue;                                   // dropped for every d
+                int mx = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) mx = max(mx, (int)((word >> (8 + 6 * b)) & 63));
+                R = max(R, dw);
+                T = max(T, mx << (W4 - dw));
+            }
+        }
+        R = max(R, __shfl_xor(R, 1, 64));
+        T = max(T, __shfl_xor(T, 1, 64));
+        // the largest |w''| of the row: max over live groups of m 2^(R - dw) * MAGMAX
+        const int need = plainw ? MAGMAX : (T >> (W4 - R)) * MAGMAX;
+        uint32_t bad = need > 32256 ? 1u : 0u;
+        for (int o = 32; o > 0; o >>= 1) bad |= __shfl_xor(bad, o, 64);
+        if (h == 0) sR[r] = R;
+        if (lane == 0) sFlag[wid] = bad;
+    }
+    __syncthreads();
+    const uint32_t dall = sFlag[0] | sFlag[1] | sFlag[2] | sFlag[3];
+    const bool wide = (sFlag[4] | sFlag[5] | sFlag[6] | sFlag[7]) != 0;
+    const uint32_t dm = dall & ((1u << (W4 + 1)) - 1);
+    const bool over = (dall >> 31) != 0;
+    const int np = __builtin_popcount(dm);
+    const int dmin = dm ? __builtin_ctz(dm) : 0, dmax = dm ? 31 - __builtin_clz(dm) : 0;
+    // Horner over the planes in int32: |sum_p 2^(dmax - d_p) C_p| <= K 127 128 (2^(dmax - dmin + 1) - 1)
+    const bool fits = dm && (int64_t)a.K * 127 * 128 * ((2ll << (dmax - dmin)) - 1) < (1ll << 31);
+    const bool single = np == 1 && !over;
+
+    if (dm == 0 || !fits || wide) {
+        // every group drops (acc 0), or the exact VALU path
+        for (int idx = tid; idx < TM * TN; idx += 512) {
+            const int r = idx / TN, c = idx % TN, m = m0 + r, n = n0 + c;
+            if (m >= a.M || n >= a.N) continue;
+            const int64_t acc = dm ? valu_acc4<FMT>(a, m, n, plainw) : 0;
+            const float sw = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(a.ws + (int64_t)n * a.srs));
+            store_out(a, m, n, acc, sw, sSa2[r]);
+        }
+        return;
+    }
+
+    int8_t* const ringA = lds;
+    int8_t* const ringR = lds + OFF_RAW;
+    int8_t* const planes = lds + OFF_PL;        // [buffer][plane][128 x 128]
+
+    // ---- the streaming waves' sources (per lane) ----
+    const int hw = wid & 3;
+    const int8_t* srcA[DMA_A];
+    const uint8_t* srcB[2];
+    const uint8_t* srcW;                        // the dword a lane loads a raw stage (stride per stage below)
+    int64_t stepW = 0;
+    if (streamer) {
+#pragma unroll
+        for (int u = 0; u < DMA_A; ++u) {
+            const int blk = hw * DMA_A + u, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ rswz(r);
+            srcA[u] = a.q + (int64_t)min(m0 + r, a.M - 1) * a.ldq + 16 * c;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int blk = hw * 2 + u, r = blk * 16 + (lane >> 2), c = lane & 3;
+            srcB[u] = a.w + (int64_t)min(n0 + r, a.N - 1) * a.rs + 16 * c;
+        }
+        const int r = (hw & 1) * 64 + lane;
+        if (hw < 2) {                           // the weight rows' scale words (a dummy for UNIT / RSC)
+            srcW = plainw ? reinterpret_cast<const uint8_t*>(a.q)
+                          : a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
+            stepW = plainw ? 0 : 4;
+        } else {                                // the activation rows' offset words
+            srcW = a.da + (int64_t)min(m0 + r, a.M - 1) * a.ldda;
+            stepW = 4;
+        }
+    }
+    auto issue_a = [&](int s) {
+        const uint32_t base = lds_addr(ringA + (s % NA) * ATILE) + hw * DMA_A * 1024;
+#pragma unroll
+        for (int u = 0; u < DMA_A; ++u) dma16(srcA[u] + s * BK, base + 1024u * u);
+    };
+    auto issue_r = [&](int s) {
+        const uint32_t base = lds_addr(ringR + (s % NR) * RSLOT);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) dma16(srcB[u] + s * (BK / 2), base + (uint32_t)(hw * 2 + u) * 1024u);
+        dma4(srcW + s * stepW, base + (uint32_t)RAWB + (uint32_t)hw * 256u);
+    };
+    // vmcnt(n) for the counts a walk can leave outstanding (n a multiple of 3 or 4 up to 14)
+    auto wait_n = [&](int n) {
+        switch (n) {
+            case 14: wait_vm<14>(); break;
+            case 11: wait_vm<11>(); break;
+            case 10: wait_vm<10>(); break;
+            case 7: wait_vm<7>(); break;
+            case 4: wait_vm<4>(); break;
+            case 3: wait_vm<3>(); break;
+            default: wait_vm<0>(); break;
+        }
+    };
+    // the expansion of raw stage s into plane buffer s & 1 for activation plane d (streaming thread
+    // (row r, half h): the row's 64 elements of its half, two 32-groups)
+    const int er = (tid - 256) >> 1, eh = tid & 1;
+    // (the two groups in a rolled loop: the kernel runs once a CU from a cold instruction cache,
+    // so the code's length is part of its latency)
+    auto expand = [&](int s, int d) {
+        const int8_t* slot = ringR + (s % NR) * RSLOT;
+        const uint32_t word = *reinterpret_cast<const uint32_t*>(slot + RAWB + 4 * er);
+        const int R = sR[er];
+        const int dw = HI ? (int)(word & 0xFF) : 0;
+        const bool live = dw + d <= W4;
+        int8_t* pl = planes + (s & 1) * 2 * PLANE;
+#pragma unroll 1
+        for (int g = 0; g < 2; ++g) {
+            const uint4 x = *reinterpret_cast<const uint4*>(slot + er * 64 + 32 * eh + 16 * g);
+            const int b = 2 * eh + g;
+            const int m = HI ? (int)((word >> (8 + 6 * b)) & 63) : 1;
+            const int mp = live ? m << (R - dw) : 0;
+            uint32_t tl[4], th[4];
+            group_tables<FMT>(mp, tl, th);
+            uint32_t l[8], hv[8];
+            expand8<HI>(x.x, tl, th, l[0], l[1], hv[0], hv[1]);
+            expand8<HI>(x.y, tl, th, l[2], l[3], hv[2], hv[3]);
+            expand8<HI>(x.z, tl, th, l[4], l[5], hv[4], hv[5]);
+            expand8<HI>(x.w, tl, th, l[6], l[7], hv[6], hv[7]);
+            const int c0 = 4 * eh + 2 * g;      // the group's two 16-byte chunks
+            *reinterpret_cast<uint4*>(pl + rof(er, c0)) = make_uint4(l[0], l[1], l[2], l[3]);
+            *reinterpret_cast<uint4*>(pl + rof(er, c0 + 1)) = make_uint4(l[4], l[5], l[6], l[7]);
+            if (HI) {
+                *reinterpret_cast<uint4*>(pl + PLANE + rof(er, c0)) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+                *reinterpret_cast<uint4*>(pl + PLANE + rof(er, c0 + 1)) = make_uint4(hv[4], hv[5], hv[6], hv[7]);
+            }
+        }
+    };
+
+    if (streamer) {
+        for (uint32_t left = dm; left; left &= left - 1) {     // the activation planes in ascending d
+            const int d = __builtin_ctz(left);
+            // prologue: raw 0, then (A 0, raw 1), (A 1, raw 2)
+            issue_r(0);
+            if (KS > 1) { issue_a(0); issue_r(1); } else { issue_a(0); }
+            if (KS > 2) { issue_a(1); issue_r(2); } else if (KS > 1) { issue_a(1); }
+            // raw 0 landed: younger than it the (A 0, raw 1) and (A 1, raw 2) issued
+            wait_n((KS > 1 ? DMA_A + DMA_R : DMA_A) + (KS > 2 ? DMA_A + DMA_R : (KS > 1 ? DMA_A : 0)));
+            bar();                              // every stream wave's raw 0 (and the planes' last reads)
+            expand(0, d);
+            // raw 1 and A 0 landed: younger than raw 1 the (A 1, raw 2)
+            wait_n(KS > 2 ? DMA_A + DMA_R : (KS > 1 ? DMA_A : 0));
+            bar();                              // stage 0 ready
+            for (int kt = 0; kt < KS; ++kt) {
+                int n = 0;
+                if (kt + 2 < KS) { issue_a(kt + 2); n += DMA_A; }
+                if (kt + 3 < KS) { issue_r(kt + 3); n += DMA_R; }
+                if (kt + 1 < KS) expand(kt + 1, d);
+                wait_n(n);                      // raw kt + 2 and A kt + 1 landed
+                bar();                          // stage kt + 1 ready (or the walk's end)
+            }
+        }
+        return;
+    }
+
+    const int wm = wid >> 1, wn = wid & 1;
+    v4i accl[4][4], acch[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) accl[i][j] = acch[i][j] = v4i{0, 0, 0, 0};
+    int dprev = -1;
+    for (uint32_t left = dm; left; left &= left - 1) {         // the activation planes in ascending d
+        const int d = __builtin_ctz(left);
+        if (dprev >= 0) {                       // Horner: room for this plane
+            const int gap = d - dprev;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    accl[i][j] = accl[i][j] << gap;
+                    acch[i][j] = acch[i][j] << gap;
+                }
+        }
+        bar();                                  // the streamers' raw 0
+        bar();                                  // stage 0 ready
+        for (int kt = 0; kt < KS; ++kt) {
+            const int8_t* A = ringA + (kt % NA) * ATILE;
+            const int8_t* PL = planes + (kt & 1) * 2 * PLANE;
+            const uint32_t* daw = reinterpret_cast<const uint32_t*>(ringR + (kt % NR) * RSLOT + RAWB + 512);
+            uint32_t dwd[4] = {0u, 0u, 0u, 0u};
+            if (!single) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dwd[i] = daw[wm * 64 + i * 16 + (lane & 15)];
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int c = ks * 4 + (lane >> 4);
+                const int gsh = 8 * (c >> 1);
+                v4i fa[4], fl[4], fh[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v4i v = *reinterpret_cast<const v4i*>(A + rof(wm * 64 + i * 16 + (lane & 15), c));
+                    if (!single && ((dwd[i] >> gsh) & 0xFFu) != (uint32_t)d) v = v4i{0, 0, 0, 0};
+                    fa[i] = v;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int ro = rof(wn * 64 + j * 16 + (lane & 15), c);
+                    fl[j] = *reinterpret_cast<const v4i*>(PL + ro);
+                    if (HI) fh[j] = *reinterpret_cast<const v4i*>(PL + PLANE + ro);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        accl[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fl[j], accl[i][j], 0, 0, 0);
+                        if (HI) acch[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fh[j], acch[i][j], 0, 0, 0);
+                    }
+            }
+            bar();                              // stage kt + 1 ready (or the walk's end)
+        }
+        dprev = d;
+    }
+
+    // ---- epilogue: T = 256 C_h + C_l, acc = T 2^(11 - R_n - dmax), the fp32 epilogue ----
+    // Each wave's two planes of sums go to LDS column-major (the four rows an MFMA lane holds
+    // are contiguous: one 16-byte write each), then a rolled loop over the wave's 16 row groups
+    // (lane: row 4 s + lane / 16, columns 4 (lane & 15) .. + 3) forms each output and stores 4
+    // columns at once.  acc < 2^47 converts to double exactly, and cvt_f32_f64 rounds it as
+    // i2f does (nearest even).
+    int* Tl = reinterpret_cast<int*>(lds) + wid * 2 * 64 * TPS;   // [column][row], TPS apart
+    int* Th = Tl + 64 * TPS;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int o = (16 * j + (lane & 15)) * TPS + 16 * i + 4 * (lane >> 4);
+            *reinterpret_cast<v4i*>(Tl + o) = accl[i][j];
+            if (HI) *reinterpret_cast<v4i*>(Th + o) = acch[i][j];
+        }
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");   // this wave's writes done
+    const int q = lane & 15;
+    const int nc = n0 + wn * 64 + 4 * q;           // this lane's four columns
+    float sw[4];
+    int sh[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int n = min(nc + c, a.N - 1);
+        sw[c] = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(a.ws + (int64_t)n * a.srs));
+        sh[c] = W4 - sR[n - n0] - dmax;
+    }
+    const bool full = m0 + TM <= a.M && n0 + TN <= a.N && a.vec4;
+    const bool asc = (a.flags & OTPU_ASCALE) != 0, accf = (a.flags & OTPU_ACC) != 0;
+#pragma unroll 1
+    for (int sgrp = 0; sgrp < 16; ++sgrp) {
+        const int r = 4 * sgrp + (lane >> 4);      // the wave's row
+        const int m = m0 + wm * 64 + r;
+        const float sa = sSa2[wm * 64 + r];
+        float y[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int o = (4 * q + c) * TPS + r;
+            const int64_t T = (HI ? (int64_t)Th[o] * 256 : 0) + (int64_t)Tl[o];
+            const int64_t acc = sh[c] >= 0 ? T * ((int64_t)1 << sh[c]) : T >> (-sh[c]);
+            y[c] = fmul_f(fmul_f((float)(double)acc, sw[c]), sa);
+        }
+        float* p = a.out + (int64_t)m * a.ors + nc;
+        if (full) {
+            if (asc || accf) {
+                const float4 old = *reinterpret_cast<const float4*>(p);
+                const float ov[4] = {old.x, old.y, old.z, old.w};
+                const float al = asc ? a.alpha[m] : 1.0f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) y[c] = asc ? fadd(fmul(ov[c], al), y[c]) : fadd(ov[c], y[c]);
+            }
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            __builtin_nontemporal_store(f32x4{y[0], y[1], y[2], y[3]}, reinterpret_cast<f32x4*>(p));
+        } else if (m < a.M) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                if (nc + c >= a.N) continue;
+                float v = y[c];
+                if (asc) v = fadd(fmul(p[c], a.alpha[m]), v);
+                else if (accf) v = fadd(p[c], v);
+                p[c] = v;
+            }
+        }
+    }
+}
+
+}  // namespace g4
+}  // namespace otpu
+
+using namespace otpu;
+
+// returns 1 when the call is not for this kernel (otpu_mm then streams it), else a status
+int otpu_gemm4_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda, int M, int K,
+                   const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
+                   const float* alpha, float* out, int64_t ors, hipStream_t s) {
+    if ((fmt != OTPU_INT4 && fmt != OTPU_FP4) || M < 16 || (flags & OTPU_RMAX)) return 1;
+    if (((uintptr_t)da & 3) || (ldda % 4) || ((uintptr_t)q & 15) || (ldq % 16) || ((uintptr_t)w & 15) || (rs % 16))
+        return 1;
+    if (!(flags & OTPU_UNIT) && (((uintptr_t)ws & 3) || (srs % 4))) return 1;
+    g4::Args a = {};
+    a.q = q; a.ldq = ldq; a.Sa = Sa; a.da = da; a.ldda = ldda; a.M = M; a.K = K;
+    a.w = w; a.rs = rs; a.ws = ws; a.srs = srs; a.N = N; a.flags = flags; a.k0 = k0;
+    a.alpha = alpha; a.out = out; a.ors = ors;
+    a.tiles_m = (M + g4::TM - 1) / g4::TM;
+    a.tiles_n = (N + g4::TN - 1) / g4::TN;
+    a.vec4 = ((uintptr_t)out % 16 == 0) && (ors % 4 == 0);
+    const unsigned grid = (unsigned)(a.tiles_m * a.tiles_n);
+    const bool hi = !(flags & (OTPU_UNIT | OTPU_RSC));
+    if (fmt == OTPU_INT4) {
+        if (hi) g4::gemm4_kernel<OTPU_INT4, true><<<grid, 512, 0, s>>>(a);
+        else g4::gemm4_kernel<OTPU_INT4, false><<<grid, 512, 0, s>>>(a);
+    } else {
+        if (hi) g4::gemm4_kernel<OTPU_FP4, true><<<grid, 512, 0, s>>>(a);
+        else g4::gemm4_kernel<OTPU_FP4, false><<<grid, 512, 0, s>>>(a);
+    }
+    return otpu_launch_check("mm gemm4");
+}

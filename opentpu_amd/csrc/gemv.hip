@@ -171,6 +171,9 @@ static MMArgs make_args(const int8_t* q, int64_t ldq, const float* Sa, const uin
 int otpu_gemm_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda, int M, int K,
                   const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
                   const float* alpha, float* out, int64_t ors, hipStream_t s);
+int otpu_gemm4_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda, int M, int K,
+                   const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
+                   const float* alpha, float* out, int64_t ors, hipStream_t s);
 
 extern "C" int otpu_mm(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda,
                        int M, int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N,
@@ -186,6 +189,9 @@ extern "C" int otpu_mm(const int8_t* q, int64_t ldq, const float* Sa, const uint
         rc = otpu_gemm_try(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, fmt, flags & ~OTPU_PAIR, k0, alpha,
                            out, ors, s);
         if (rc <= 0) return rc;                       // handled (or failed); > 0: not this path
+        rc = otpu_gemm4_try(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, fmt, flags & ~OTPU_PAIR, k0, alpha,
+                            out, ors, s);
+        if (rc <= 0) return rc;
     }
     MMArgs a = make_args(q, ldq, Sa, da, ldda, M, K, w, rs, ws, srs, N, flags, k0);
     a.alpha = alpha; a.out = out; a.ors = ors;
