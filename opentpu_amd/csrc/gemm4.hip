@@ -216,6 +216,80 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     const int KS = a.K / BK;
     constexpr int MAGMAX = FMT == OTPU_INT4 ? 8 : 12;
 
+    // ---- the streams' sources, and the first walk's first loads (before the scan, whose
+    // latency they then overlap) ----
+    int8_t* const ringA = lds;
+    int8_t* const ringR = lds + OFF_RAW;
+    int8_t* const planes = lds + OFF_PL;        // [buffer][plane][128 x 128]
+
+    // ---- the streaming waves' sources (per lane) ----
+    const int hw = wid & 3;
+    const int8_t* srcA[DMA_A];
+    const uint8_t* srcB[2];
+    const uint8_t* srcW;                        // the dword a lane loads a raw stage (stride per stage below)
+    int64_t stepW = 0;
+    if (streamer) {
+#pragma unroll
+        for (int u = 0; u < DMA_A; ++u) {
+            const int blk = hw * DMA_A + u, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ rswz(r);
+            srcA[u] = a.q + (int64_t)min(m0 + r, a.M - 1) * a.ldq + 16 * c;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int blk = hw * 2 + u, r = blk * 16 + (lane >> 2), c = lane & 3;
+            srcB[u] = a.w + (int64_t)min(n0 + r, a.N - 1) * a.rs + 16 * c;
+        }
+        const int r = (hw & 1) * 64 + lane;
+        if (hw < 2) {                           // the weight rows' scale words (a dummy for UNIT / RSC)
+            srcW = plainw ? reinterpret_cast<const uint8_t*>(a.q)
+                          : a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
+            stepW = plainw ? 0 : 4;
+        } else {                                // the activation rows' offset words
+            srcW = a.da + (int64_t)min(m0 + r, a.M - 1) * a.ldda;
+            stepW = 4;
+        }
+    }
+    auto issue_a = [&](int s) {
+        const uint32_t base = lds_addr(ringA + (s % NA) * ATILE) + hw * DMA_A * 1024;
+#pragma unroll
+        for (int u = 0; u < DMA_A; ++u) dma16(srcA[u] + s * BK, base + 1024u * u);
+    };
+    auto issue_r = [&](int s) {
+        const uint32_t base = lds_addr(ringR + (s % NR) * RSLOT);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) dma16(srcB[u] + s * (BK / 2), base + (uint32_t)(hw * 2 + u) * 1024u);
+        dma4(srcW + s * stepW, base + (uint32_t)RAWB + (uint32_t)hw * 256u);
+    };
+    // vmcnt(n) for the counts a walk can leave outstanding (n a multiple of 3 or 4 up to 14)
+    auto wait_n = [&](int n) {
+        switch (n) {
+            case 14: wait_vm<14>(); break;
+            case 11: wait_vm<11>(); break;
+            case 10: wait_vm<10>(); break;
+            case 7: wait_vm<7>(); break;
+            case 4: wait_vm<4>(); break;
+            case 3: wait_vm<3>(); break;
+            default: wait_vm<0>(); break;
+        }
+    };
+    // the expansion of raw stage s into plane buffer s & 1 for activation plane d (streaming thread
+    // (row r, half h): the row's 64 elements of its half, two 32-groups)
+    auto prologue_issue = [&] {                 // raw 0, then (A 0, raw 1), (A 1, raw 2)
+        issue_r(0);
+        if (KS > 1) { issue_a(0); issue_r(1); } else { issue_a(0); }
+        if (KS > 2) { issue_a(1); issue_r(2); } else if (KS > 1) { issue_a(1); }
+    };
+    // the epilogue's column scales (region wid & 3's columns), loaded before any stream (a stream
+    // wave's waits count only the loads issued after them)
+    const int q = lane & 15;
+    const int wm = (wid & 3) >> 1, wn = wid & 1;
+    const int nc = n0 + wn * 64 + 4 * q;           // this lane's four epilogue columns
+    float sw[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        sw[c] = unit ? 1.0f : *reinterpret_cast<const float*>(a.ws + (int64_t)min(nc + c, a.N - 1) * a.srs);
+    if (streamer) prologue_issue();
+
     // ---- the tile's scan: activation offsets (waves 0-3), weight offsets and multipliers (4-7) ----
     if (!streamer) {
         if (tid < TM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-W4)) : 0.0f;
@@ -276,6 +350,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 
     if (dm == 0 || !fits || wide) {
         // every group drops (acc 0), or the exact VALU path
+        if (streamer) wait_vm<0>();             // (the first walk's loads, issued before the scan)
         for (int idx = tid; idx < TM * TN; idx += 512) {
             const int r = idx / TN, c = idx % TN, m = m0 + r, n = n0 + c;
             if (m >= a.M || n >= a.N) continue;
@@ -286,78 +361,23 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         return;
     }
 
-    int8_t* const ringA = lds;
-    int8_t* const ringR = lds + OFF_RAW;
-    int8_t* const planes = lds + OFF_PL;        // [buffer][plane][128 x 128]
-
-    // ---- the streaming waves' sources (per lane) ----
-    const int hw = wid & 3;
-    const int8_t* srcA[DMA_A];
-    const uint8_t* srcB[2];
-    const uint8_t* srcW;                        // the dword a lane loads a raw stage (stride per stage below)
-    int64_t stepW = 0;
-    if (streamer) {
-#pragma unroll
-        for (int u = 0; u < DMA_A; ++u) {
-            const int blk = hw * DMA_A + u, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ rswz(r);
-            srcA[u] = a.q + (int64_t)min(m0 + r, a.M - 1) * a.ldq + 16 * c;
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int blk = hw * 2 + u, r = blk * 16 + (lane >> 2), c = lane & 3;
-            srcB[u] = a.w + (int64_t)min(n0 + r, a.N - 1) * a.rs + 16 * c;
-        }
-        const int r = (hw & 1) * 64 + lane;
-        if (hw < 2) {                           // the weight rows' scale words (a dummy for UNIT / RSC)
-            srcW = plainw ? reinterpret_cast<const uint8_t*>(a.q)
-                          : a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
-            stepW = plainw ? 0 : 4;
-        } else {                                // the activation rows' offset words
-            srcW = a.da + (int64_t)min(m0 + r, a.M - 1) * a.ldda;
-            stepW = 4;
-        }
-    }
-    auto issue_a = [&](int s) {
-        const uint32_t base = lds_addr(ringA + (s % NA) * ATILE) + hw * DMA_A * 1024;
-#pragma unroll
-        for (int u = 0; u < DMA_A; ++u) dma16(srcA[u] + s * BK, base + 1024u * u);
-    };
-    auto issue_r = [&](int s) {
-        const uint32_t base = lds_addr(ringR + (s % NR) * RSLOT);
-#pragma unroll
-        for (int u = 0; u < 2; ++u) dma16(srcB[u] + s * (BK / 2), base + (uint32_t)(hw * 2 + u) * 1024u);
-        dma4(srcW + s * stepW, base + (uint32_t)RAWB + (uint32_t)hw * 256u);
-    };
-    // vmcnt(n) for the counts a walk can leave outstanding (n a multiple of 3 or 4 up to 14)
-    auto wait_n = [&](int n) {
-        switch (n) {
-            case 14: wait_vm<14>(); break;
-            case 11: wait_vm<11>(); break;
-            case 10: wait_vm<10>(); break;
-            case 7: wait_vm<7>(); break;
-            case 4: wait_vm<4>(); break;
-            case 3: wait_vm<3>(); break;
-            default: wait_vm<0>(); break;
-        }
-    };
-    // the expansion of raw stage s into plane buffer s & 1 for activation plane d (streaming thread
-    // (row r, half h): the row's 64 elements of its half, two 32-groups)
-    const int er = (tid - 256) >> 1, eh = tid & 1;
     // (the two groups in a rolled loop: the kernel runs once a CU from a cold instruction cache,
     // so the code's length is part of its latency)
+    // Thread t expands 32-groups gi = t and t + 256 of the stage (group gi: row gi / 4, its
+    // group gi % 4): each read instruction then reads 1 KB of raw nibbles contiguously, free of
+    // bank conflicts (a thread per half row read 32-byte strided lanes: 8-way conflicts).
     auto expand = [&](int s, int d) {
         const int8_t* slot = ringR + (s % NR) * RSLOT;
-        const uint32_t word = *reinterpret_cast<const uint32_t*>(slot + RAWB + 4 * er);
-        const int R = sR[er];
-        const int dw = HI ? (int)(word & 0xFF) : 0;
-        const bool live = dw + d <= W4;
         int8_t* pl = planes + (s & 1) * 2 * PLANE;
 #pragma unroll 1
-        for (int g = 0; g < 2; ++g) {
-            const uint4 x = *reinterpret_cast<const uint4*>(slot + er * 64 + 32 * eh + 16 * g);
-            const int b = 2 * eh + g;
+        for (int gi = tid - 256; gi < 512; gi += 256) {
+            const int row = gi >> 2, b = gi & 3;
+            const uint4 x = *reinterpret_cast<const uint4*>(slot + 16 * gi);
+            const uint32_t word = *reinterpret_cast<const uint32_t*>(slot + RAWB + 4 * row);
+            const int R = sR[row];
+            const int dw = HI ? (int)(word & 0xFF) : 0;
             const int m = HI ? (int)((word >> (8 + 6 * b)) & 63) : 1;
-            const int mp = live ? m << (R - dw) : 0;
+            const int mp = dw + d <= W4 ? m << (R - dw) : 0;
             uint32_t tl[4], th[4];
             group_tables<FMT>(mp, tl, th);
             uint32_t l[8], hv[8];
@@ -365,12 +385,11 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
             expand8<HI>(x.y, tl, th, l[2], l[3], hv[2], hv[3]);
             expand8<HI>(x.z, tl, th, l[4], l[5], hv[4], hv[5]);
             expand8<HI>(x.w, tl, th, l[6], l[7], hv[6], hv[7]);
-            const int c0 = 4 * eh + 2 * g;      // the group's two 16-byte chunks
-            *reinterpret_cast<uint4*>(pl + rof(er, c0)) = make_uint4(l[0], l[1], l[2], l[3]);
-            *reinterpret_cast<uint4*>(pl + rof(er, c0 + 1)) = make_uint4(l[4], l[5], l[6], l[7]);
+            *reinterpret_cast<uint4*>(pl + rof(row, 2 * b)) = make_uint4(l[0], l[1], l[2], l[3]);
+            *reinterpret_cast<uint4*>(pl + rof(row, 2 * b + 1)) = make_uint4(l[4], l[5], l[6], l[7]);
             if (HI) {
-                *reinterpret_cast<uint4*>(pl + PLANE + rof(er, c0)) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
-                *reinterpret_cast<uint4*>(pl + PLANE + rof(er, c0 + 1)) = make_uint4(hv[4], hv[5], hv[6], hv[7]);
+                *reinterpret_cast<uint4*>(pl + PLANE + rof(row, 2 * b)) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+                *reinterpret_cast<uint4*>(pl + PLANE + rof(row, 2 * b + 1)) = make_uint4(hv[4], hv[5], hv[6], hv[7]);
             }
         }
     };
@@ -378,10 +397,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     if (streamer) {
         for (uint32_t left = dm; left; left &= left - 1) {     // the activation planes in ascending d
             const int d = __builtin_ctz(left);
-            // prologue: raw 0, then (A 0, raw 1), (A 1, raw 2)
-            issue_r(0);
-            if (KS > 1) { issue_a(0); issue_r(1); } else { issue_a(0); }
-            if (KS > 2) { issue_a(1); issue_r(2); } else if (KS > 1) { issue_a(1); }
+            if (left != dm) prologue_issue();   // (the first plane's: before the scan)
             // raw 0 landed: younger than it the (A 0, raw 1) and (A 1, raw 2) issued
             wait_n((KS > 1 ? DMA_A + DMA_R : DMA_A) + (KS > 2 ? DMA_A + DMA_R : (KS > 1 ? DMA_A : 0)));
             bar();                              // every stream wave's raw 0 (and the planes' last reads)
@@ -398,17 +414,14 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
                 bar();                          // stage kt + 1 ready (or the walk's end)
             }
         }
-        return;
     }
-
-    const int wm = wid >> 1, wn = wid & 1;
     v4i accl[4][4], acch[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) accl[i][j] = acch[i][j] = v4i{0, 0, 0, 0};
     int dprev = -1;
-    for (uint32_t left = dm; left; left &= left - 1) {         // the activation planes in ascending d
+    for (uint32_t left = streamer ? 0u : dm; left; left &= left - 1) {   // the planes in ascending d
         const int d = __builtin_ctz(left);
         if (dprev >= 0) {                       // Horner: room for this plane
             const int gap = d - dprev;
@@ -431,31 +444,35 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) dwd[i] = daw[wm * 64 + i * 16 + (lane & 15)];
             }
+            // every fragment of the stage read before its MFMAs (per 64-deep step, the reads and
+            // the MFMAs behind them ran in series)
+            v4i fa[2][4], fl[2][4], fh[2][4];
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const int c = ks * 4 + (lane >> 4);
                 const int gsh = 8 * (c >> 1);
-                v4i fa[4], fl[4], fh[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     v4i v = *reinterpret_cast<const v4i*>(A + rof(wm * 64 + i * 16 + (lane & 15), c));
                     if (!single && ((dwd[i] >> gsh) & 0xFFu) != (uint32_t)d) v = v4i{0, 0, 0, 0};
-                    fa[i] = v;
+                    fa[ks][i] = v;
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int ro = rof(wn * 64 + j * 16 + (lane & 15), c);
-                    fl[j] = *reinterpret_cast<const v4i*>(PL + ro);
-                    if (HI) fh[j] = *reinterpret_cast<const v4i*>(PL + PLANE + ro);
+                    fl[ks][j] = *reinterpret_cast<const v4i*>(PL + ro);
+                    if (HI) fh[ks][j] = *reinterpret_cast<const v4i*>(PL + PLANE + ro);
                 }
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        accl[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fl[j], accl[i][j], 0, 0, 0);
-                        if (HI) acch[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fh[j], acch[i][j], 0, 0, 0);
+                        accl[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[ks][i], fl[ks][j], accl[i][j], 0, 0, 0);
+                        if (HI) acch[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[ks][i], fh[ks][j], acch[i][j], 0, 0, 0);
                     }
-            }
             bar();                              // stage kt + 1 ready (or the walk's end)
         }
         dprev = d;
@@ -467,32 +484,33 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     // (lane: row 4 s + lane / 16, columns 4 (lane & 15) .. + 3) forms each output and stores 4
     // columns at once.  acc < 2^47 converts to double exactly, and cvt_f32_f64 rounds it as
     // i2f does (nearest even).
-    int* Tl = reinterpret_cast<int*>(lds) + wid * 2 * 64 * TPS;   // [column][row], TPS apart
+    // (full tiles: wave w stores row groups 0-7 of region w, stream wave w + 4 groups 8-15)
+    const int region = wid & 3;
+    int* Tl = reinterpret_cast<int*>(lds) + region * 2 * 64 * TPS;   // [column][row], TPS apart
     int* Th = Tl + 64 * TPS;
+    if (!streamer) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int o = (16 * j + (lane & 15)) * TPS + 16 * i + 4 * (lane >> 4);
-            *reinterpret_cast<v4i*>(Tl + o) = accl[i][j];
-            if (HI) *reinterpret_cast<v4i*>(Th + o) = acch[i][j];
-        }
-    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");   // this wave's writes done
-    const int q = lane & 15;
-    const int nc = n0 + wn * 64 + 4 * q;           // this lane's four columns
-    float sw[4];
+            for (int j = 0; j < 4; ++j) {
+                const int o = (16 * j + (lane & 15)) * TPS + 16 * i + 4 * (lane >> 4);
+                *reinterpret_cast<v4i*>(Tl + o) = accl[i][j];
+                if (HI) *reinterpret_cast<v4i*>(Th + o) = acch[i][j];
+            }
+    }
+    __syncthreads();                                // the transposes written
     int sh[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        const int n = min(nc + c, a.N - 1);
-        sw[c] = unit ? 1.0f : ftz(*reinterpret_cast<const float*>(a.ws + (int64_t)n * a.srs));
-        sh[c] = W4 - sR[n - n0] - dmax;
+        sw[c] = ftz(sw[c]);
+        sh[c] = W4 - sR[min(nc + c, a.N - 1) - n0] - dmax;
     }
     const bool full = m0 + TM <= a.M && n0 + TN <= a.N && a.vec4;
     const bool asc = (a.flags & OTPU_ASCALE) != 0, accf = (a.flags & OTPU_ACC) != 0;
+    const int s0 = streamer ? 8 : 0;
 #pragma unroll 1
-    for (int sgrp = 0; sgrp < 16; ++sgrp) {
-        const int r = 4 * sgrp + (lane >> 4);      // the wave's row
+    for (int sgrp = s0; sgrp < s0 + 8; ++sgrp) {
+        const int r = 4 * sgrp + (lane >> 4);      // the region's row
         const int m = m0 + wm * 64 + r;
         const float sa = sSa2[wm * 64 + r];
         float y[4];
