@@ -363,15 +363,16 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 
     // (the two groups in a rolled loop: the kernel runs once a CU from a cold instruction cache,
     // so the code's length is part of its latency)
-    // Thread t expands 32-groups gi = t and t + 256 of the stage (group gi: row gi / 4, its
-    // group gi % 4): each read instruction then reads 1 KB of raw nibbles contiguously, free of
-    // bank conflicts (a thread per half row read 32-byte strided lanes: 8-way conflicts).
+    // Every thread of the workgroup expands one of the stage's 512 32-groups, gi = its thread
+    // index (row gi / 4, the row's group gi % 4): the multiplying waves do theirs behind their
+    // MFMAs, whose matrix pipe runs beside the VALU (the streaming waves alone, two groups a
+    // thread, took ~1.4 us a stage, latency-bound).  A read instruction reads 1 KB of raw nibbles
+    // contiguously, free of bank conflicts.
     auto expand = [&](int s, int d) {
         const int8_t* slot = ringR + (s % NR) * RSLOT;
         int8_t* pl = planes + (s & 1) * 2 * PLANE;
-#pragma unroll 1
-        for (int gi = tid - 256; gi < 512; gi += 256) {
-            const int row = gi >> 2, b = gi & 3;
+        {
+            const int gi = tid, row = gi >> 2, b = gi & 3;
             const uint4 x = *reinterpret_cast<const uint4*>(slot + 16 * gi);
             const uint32_t word = *reinterpret_cast<const uint32_t*>(slot + RAWB + 4 * row);
             const int R = sR[row];
@@ -434,6 +435,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
                 }
         }
         bar();                                  // the streamers' raw 0
+        expand(0, d);
         bar();                                  // stage 0 ready
         for (int kt = 0; kt < KS; ++kt) {
             const int8_t* A = ringA + (kt % NA) * ATILE;
@@ -473,6 +475,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
                         accl[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[ks][i], fl[ks][j], accl[i][j], 0, 0, 0);
                         if (HI) acch[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[ks][i], fh[ks][j], acch[i][j], 0, 0, 0);
                     }
+            if (kt + 1 < KS) expand(kt + 1, d);  // (raw kt + 1 landed before this stage's barrier)
             bar();                              // stage kt + 1 ready (or the walk's end)
         }
         dprev = d;
