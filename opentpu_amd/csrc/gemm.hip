@@ -184,9 +184,10 @@ __device__ __forceinline__ RingSrc ring_src(const GemmArgs& a, const int8_t* rin
     return rs;
 }
 
-__device__ __forceinline__ void ring_issue(const RingSrc& rs, int kt) {
+// walk step kt into its ring slot; dk: the K stage it holds (kt, or kt rotated: see lw_rot)
+__device__ __forceinline__ void ring_issue(const RingSrc& rs, int kt, int dk) {
     const uint32_t sl = rs.base + (uint32_t)((kt % NS) * STAGE);
-    const int o = kt * RBK;
+    const int o = dk * RBK;
 #pragma unroll
     for (int u = 0; u < LPS / 2; ++u) dma16(rs.ga[u] + o, sl + 1024u * u);
 #pragma unroll
@@ -200,7 +201,7 @@ __device__ __forceinline__ void ring_prologue(const GemmArgs& a, const int8_t* r
     const int KS = a.K / RBK;
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
-        if (s < KS) ring_issue(rs, s);
+        if (s < KS) ring_issue(rs, s, s);
 }
 
 // thread t's chunk u is tile row (t + 256 u) >> 3 = (t >> 3) + 32 u, chunk t & 7
@@ -689,13 +690,22 @@ __device__ __forceinline__ int masked_barriers(int KT, uint32_t dmask, uint32_t 
 // the slot stage kt - 1 left; a compute wave arrives with its reads of stage kt - 1 done.
 // (c3 ROW x RSC: 18.5-18.7 -> 16.3-16.6 us back to back, bit-identical.)
 
+// The K walk of a tile starts at stage rot and wraps (the int32 sums are exact in any order).
+// The workgroups of one XCD run in step, so with one common order the tiles that share an A or
+// a B panel ask for each line together and all wait a miss's latency for it (L2 merges the
+// requests).  Staggered starts let one tile miss a line and the others hit it in L2 stages
+// later: the 8 tiles of an XCD that share A rows start 2 stages apart, the 4 that share B rows
+// 4 stages apart (tn & 7 and tm: the XCD-major order gives an XCD 8 consecutive column tiles).
+__device__ __forceinline__ int lw_rot(int tm, int tn, int KS) { return (2 * (tn & 7) + 4 * tm) % KS; }
+__device__ __forceinline__ int lw_stage(int kt, int rot, int KS) { return kt + rot < KS ? kt + rot : kt + rot - KS; }
+
 // a loader wave's walk (its first NS - 1 stages issued): KS + 1 barriers
-__device__ __forceinline__ void lw_load_walk(const RingSrc& rs, int KS) {
+__device__ __forceinline__ void lw_load_walk(const RingSrc& rs, int KS, int rot) {
     for (int kt = 0; kt < KS; ++kt) {
         wait_stage(min(NS - 2, KS - 1 - kt));
         ring_barrier();                                  // stage kt landed (this wave's part)
         const int nk = kt + NS - 1;
-        if (nk < KS) ring_issue(rs, nk);
+        if (nk < KS) ring_issue(rs, nk, lw_stage(nk, rot, KS));
     }
     ring_barrier();
 }
@@ -707,7 +717,7 @@ __device__ __forceinline__ void lw_load_walk(const RingSrc& rs, int KS) {
 // KS + 1 barriers, matching lw_load_walk's.
 template <int NP, bool MASK, bool ALL1 = false>
 __device__ __forceinline__ void lw_mma_walk(const int8_t* ring, const uint32_t* da_lds, v4i (&acc)[NP][4][4],
-                                            const int (&dv)[MP_MAX], int KS) {
+                                            const int (&dv)[MP_MAX], int KS, int rot) {
     const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wid >> 1, wn = wid & 1;
     for (int kt = 0; kt < KS; ++kt) {
@@ -716,8 +726,9 @@ __device__ __forceinline__ void lw_mma_walk(const int8_t* ring, const uint32_t* 
         const int8_t* B = A + TILE;
         uint32_t dw4[4] = {0u, 0u, 0u, 0u};
         if constexpr (MASK) {
+            const int dk = lw_stage(kt, rot, KS);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dw4[i] = da_lds[(wm * 64 + i * 16 + (lane & 15)) * DAS + kt];
+            for (int i = 0; i < 4; ++i) dw4[i] = da_lds[(wm * 64 + i * 16 + (lane & 15)) * DAS + dk];
         }
         v4i fa[2][4], fb[2][4];
 #pragma unroll
@@ -749,6 +760,101 @@ __device__ __forceinline__ void lw_mma_walk(const int8_t* ring, const uint32_t* 
     }
     ring_barrier();                                      // every read of the ring done
 }
+
+// the barrier of a walk whose LDS reads the compiler tracks: its own wait for every LDS read
+// (so no later wait on those reads is inserted), the barrier, and a fence that keeps the next
+// stage's reads below it
+__device__ __forceinline__ void ring_barrier_tracked() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);                  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" : : : "memory");
+}
+
+// One plane (MASK: its 32-groups, the offset d) with the fragment reads half a stage ahead.
+// A stage's fragments are two halves (K chunks 0-3 and 4-7 of its 128 bytes, 8 ds_read_b128
+// each); between barriers kt + 1 and kt + 2 a wave reads half 0 of stage kt + 1, multiplies
+// half 1 of stage kt, reads half 1 of stage kt + 1 and multiplies its half 0, so each group of
+// reads runs under 16 MFMAs (read, then multiplied, a stage took ~1000 cycles, twice the
+// MFMAs' 512).  Barrier j still follows every read of stage j - 1, so the loaders refill its
+// slot as lw_load_walk does.  KS + 1 barriers.
+struct Half {
+    v4i a[4], b[4];
+};
+
+template <bool MASK>
+__device__ __forceinline__ void lw_half_read(const int8_t* ring, const uint32_t* da_lds, Half& h, uint32_t (&dw)[4],
+                                             int kt, int ks, int KS, int rot) {
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wid >> 1, wn = wid & 1;
+    const int8_t* A = ring + (kt % NS) * STAGE;
+    const int8_t* B = A + TILE;
+    if (MASK && ks == 0) {
+        const int dk = lw_stage(kt, rot, KS);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dw[i] = da_lds[(wm * 64 + i * 16 + (lane & 15)) * DAS + dk];
+    }
+    const int c = ks * 4 + (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) h.a[i] = *reinterpret_cast<const v4i*>(A + rof(wm * 64 + i * 16 + (lane & 15), c));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h.b[j] = *reinterpret_cast<const v4i*>(B + rof(wn * 64 + j * 16 + (lane & 15), c));
+}
+
+template <bool MASK>
+__device__ __forceinline__ void lw_half_mma(const Half& h, const uint32_t (&dw)[4], v4i (&acc)[4][4], int ks, int d) {
+    const int lane = threadIdx.x & 63;
+    const int gsh = 8 * ((ks * 4 + (lane >> 4)) >> 1);
+    v4i fm[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fm[i] = !MASK || ((dw[i] >> gsh) & 0xFFu) == (uint32_t)d ? h.a[i] : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fm[i], h.b[j], acc[i][j], 0, 0, 0);
+}
+
+// (the scheduler would move the register-only MFMAs across the barriers and sink each read next
+// to its use: sched_barrier closes every region, and the group barriers keep each half's reads
+// ahead of the 16 MFMAs that hide them)
+#define OTPU_READS_THEN_MMA(nr)                                                                     \
+    do {                                                                                           \
+        if ((nr) > 8) __builtin_amdgcn_sched_group_barrier(0x100, (nr) - 8, 0);                    \
+        _Pragma("unroll") for (int g_ = 0; g_ < 8; ++g_) {                                         \
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                     \
+        }                                                                                          \
+    } while (0)
+
+template <bool MASK>
+__device__ __forceinline__ void lw_mma_walk1(const int8_t* ring, const uint32_t* da_lds, v4i (&acc)[4][4], int d,
+                                             int KS, int rot) {
+    Half h0, h1;
+    uint32_t dw[4] = {0u, 0u, 0u, 0u}, dwn[4] = {0u, 0u, 0u, 0u};
+    ring_barrier_tracked();                              // stage 0 landed everywhere
+    __builtin_amdgcn_sched_barrier(0);
+    lw_half_read<MASK>(ring, da_lds, h0, dw, 0, 0, KS, rot);
+    lw_half_read<MASK>(ring, da_lds, h1, dw, 0, 1, KS, rot);
+    lw_half_mma<MASK>(h0, dw, acc, 0, d);
+    OTPU_READS_THEN_MMA(MASK ? 20 : 16);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int kt = 0; kt + 1 < KS; ++kt) {
+        ring_barrier_tracked();                          // stage kt + 1 landed, stage kt read
+        __builtin_amdgcn_sched_barrier(0);
+        lw_half_read<MASK>(ring, da_lds, h0, dwn, kt + 1, 0, KS, rot);
+        lw_half_mma<MASK>(h1, dw, acc, 1, d);
+        OTPU_READS_THEN_MMA(MASK ? 12 : 8);
+        lw_half_read<MASK>(ring, da_lds, h1, dwn, kt + 1, 1, KS, rot);
+        lw_half_mma<MASK>(h0, dwn, acc, 0, d);
+        OTPU_READS_THEN_MMA(8);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dw[i] = dwn[i];
+    }
+    ring_barrier_tracked();                              // the walk's end
+    __builtin_amdgcn_sched_barrier(0);
+    lw_half_mma<MASK>(h1, dw, acc, 1, d);
+}
+#undef OTPU_READS_THEN_MMA
 
 // C3: a copy for the c3 prefill shape (M 512, N 8192, K 2048, dense rows, RSC scale words), its
 // sizes and strides as constants (the kernel runs once a CU from a cold instruction cache)
@@ -903,6 +1009,7 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
     const bool unit = (a.flags & OTPU_UNIT) != 0;
     const bool plain = unit || (a.flags & OTPU_RSC) != 0;
     const int KT = a.K / GBK, KS = a.K / RBK;
+    const int rot = lw_rot(tm, tn, KS);
 
     const RingSrc rs = ring_src(a, sRing, m0, n0);
     // the epilogue's column scales, loaded early (a full tile's epilogue rows are shared by
@@ -915,7 +1022,7 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
         if (split) epi_sw(a, n0, wid & 3, esw);
 #pragma unroll
         for (int s = 0; s < NS - 1; ++s)
-            if (s < KS) ring_issue(rs, s);
+            if (s < KS) ring_issue(rs, s, lw_stage(s, rot, KS));
     } else {
         if (tid < GBM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-16)) : 0.0f;
         tile_offsets(a, m0, n0, KT, plain, sDaAll, sMask);   // the offsets present in this tile
@@ -943,7 +1050,7 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
     // loader w + 4 store 8 row groups each (one more barrier for both groups)
     if (fits && (single || mp)) {
         if (loader) {
-            lw_load_walk(rs, KS);
+            lw_load_walk(rs, KS, rot);
             if (split) {
                 __syncthreads();                         // the transposes written
                 const int w = wid & 3;
@@ -974,8 +1081,8 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[0][i][j] = v4i{0, 0, 0, 0};
-            if (single) lw_mma_walk<1, false>(sRing, sDaAll, acc, dv, KS);
-            else lw_mma_walk<1, true>(sRing, sDaAll, acc, dv, KS);
+            if (single) lw_mma_walk1<false>(sRing, sDaAll, acc[0], dv[0], KS, rot);
+            else lw_mma_walk1<true>(sRing, sDaAll, acc[0], dv[0], KS, rot);
             epilogue(acc[0]);
         } else {
             v4i acc[2][4][4];
@@ -986,8 +1093,8 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) acc[p][i][j] = v4i{0, 0, 0, 0};
             // (no offsets past the window: the two planes cover every group, so plane 1 is C_all)
-            if (!over) lw_mma_walk<2, true, true>(sRing, sDaAll, acc, dv, KS);
-            else lw_mma_walk<2, true>(sRing, sDaAll, acc, dv, KS);
+            if (!over) lw_mma_walk<2, true, true>(sRing, sDaAll, acc, dv, KS, rot);
+            else lw_mma_walk<2, true>(sRing, sDaAll, acc, dv, KS, rot);
             // sum_p C_p << (smax - d_p) (the bound checked above)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
