@@ -770,13 +770,14 @@ __device__ __forceinline__ void ring_barrier_tracked() {
     asm volatile("" : : : "memory");
 }
 
-// One plane (MASK: its 32-groups, the offset d) with the fragment reads half a stage ahead.
-// A stage's fragments are two halves (K chunks 0-3 and 4-7 of its 128 bytes, 8 ds_read_b128
-// each); between barriers kt + 1 and kt + 2 a wave reads half 0 of stage kt + 1, multiplies
-// half 1 of stage kt, reads half 1 of stage kt + 1 and multiplies its half 0, so each group of
-// reads runs under 16 MFMAs (read, then multiplied, a stage took ~1000 cycles, twice the
-// MFMAs' 512).  Barrier j still follows every read of stage j - 1, so the loaders refill its
-// slot as lw_load_walk does.  KS + 1 barriers.
+// NP planes (as lw_mma_walk's; the kernels use it for one) with the fragment reads half a stage
+// ahead (for two planes it measured no faster, its accumulators spilling a few registers).  A stage's
+// fragments are two halves (K chunks 0-3 and 4-7 of its 128 bytes, 8 ds_read_b128 each);
+// between barriers kt + 1 and kt + 2 a wave reads half 0 of stage kt + 1, multiplies half 1 of
+// stage kt, reads half 1 of stage kt + 1 and multiplies its half 0, one read issued per 2 NP
+// MFMAs, so the reads run under the MFMAs (read, then multiplied, a one-plane stage took ~1000
+// cycles, twice the MFMAs' 512).  Barrier j still follows every read of stage j - 1, so the
+// loaders refill its slot as lw_load_walk does.  KS + 1 barriers.
 struct Half {
     v4i a[4], b[4];
 };
@@ -800,61 +801,69 @@ __device__ __forceinline__ void lw_half_read(const int8_t* ring, const uint32_t*
     for (int j = 0; j < 4; ++j) h.b[j] = *reinterpret_cast<const v4i*>(B + rof(wn * 64 + j * 16 + (lane & 15), c));
 }
 
-template <bool MASK>
-__device__ __forceinline__ void lw_half_mma(const Half& h, const uint32_t (&dw)[4], v4i (&acc)[4][4], int ks, int d) {
+template <int NP, bool MASK, bool ALL1>
+__device__ __forceinline__ void lw_half_mma(const Half& h, const uint32_t (&dw)[4], v4i (&acc)[NP][4][4], int ks,
+                                            const int (&dv)[MP_MAX]) {
     const int lane = threadIdx.x & 63;
     const int gsh = 8 * ((ks * 4 + (lane >> 4)) >> 1);
-    v4i fm[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fm[i] = !MASK || ((dw[i] >> gsh) & 0xFFu) == (uint32_t)d ? h.a[i] : v4i{0, 0, 0, 0};
+    for (int p = 0; p < NP; ++p) {
+        v4i fm[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+            const bool keep = !MASK || (ALL1 && p == 1) || ((dw[i] >> gsh) & 0xFFu) == (uint32_t)dv[p];
+            fm[i] = keep ? h.a[i] : v4i{0, 0, 0, 0};
+        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fm[i], h.b[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[p][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fm[i], h.b[j], acc[p][i][j], 0, 0, 0);
+    }
 }
 
 // (the scheduler would move the register-only MFMAs across the barriers and sink each read next
-// to its use: sched_barrier closes every region, and the group barriers keep each half's reads
-// ahead of the 16 MFMAs that hide them)
-#define OTPU_READS_THEN_MMA(nr)                                                                     \
+// to its use: sched_barrier closes every region, and the group barriers interleave each half's
+// reads with the MFMAs that hide them)
+#define OTPU_READS_UNDER_MMA(nr, np)                                                                \
     do {                                                                                           \
         if ((nr) > 8) __builtin_amdgcn_sched_group_barrier(0x100, (nr) - 8, 0);                    \
         _Pragma("unroll") for (int g_ = 0; g_ < 8; ++g_) {                                         \
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);                                     \
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * (np), 0);                              \
         }                                                                                          \
     } while (0)
 
-template <bool MASK>
-__device__ __forceinline__ void lw_mma_walk1(const int8_t* ring, const uint32_t* da_lds, v4i (&acc)[4][4], int d,
-                                             int KS, int rot) {
+template <int NP, bool MASK, bool ALL1 = false>
+__device__ __forceinline__ void lw_mma_walk_h(const int8_t* ring, const uint32_t* da_lds, v4i (&acc)[NP][4][4],
+                                              const int (&dv)[MP_MAX], int KS, int rot) {
     Half h0, h1;
     uint32_t dw[4] = {0u, 0u, 0u, 0u}, dwn[4] = {0u, 0u, 0u, 0u};
     ring_barrier_tracked();                              // stage 0 landed everywhere
     __builtin_amdgcn_sched_barrier(0);
     lw_half_read<MASK>(ring, da_lds, h0, dw, 0, 0, KS, rot);
     lw_half_read<MASK>(ring, da_lds, h1, dw, 0, 1, KS, rot);
-    lw_half_mma<MASK>(h0, dw, acc, 0, d);
-    OTPU_READS_THEN_MMA(MASK ? 20 : 16);
+    lw_half_mma<NP, MASK, ALL1>(h0, dw, acc, 0, dv);
+    OTPU_READS_UNDER_MMA(MASK ? 20 : 16, NP);
     __builtin_amdgcn_sched_barrier(0);
     for (int kt = 0; kt + 1 < KS; ++kt) {
         ring_barrier_tracked();                          // stage kt + 1 landed, stage kt read
         __builtin_amdgcn_sched_barrier(0);
         lw_half_read<MASK>(ring, da_lds, h0, dwn, kt + 1, 0, KS, rot);
-        lw_half_mma<MASK>(h1, dw, acc, 1, d);
-        OTPU_READS_THEN_MMA(MASK ? 12 : 8);
+        lw_half_mma<NP, MASK, ALL1>(h1, dw, acc, 1, dv);
+        OTPU_READS_UNDER_MMA(MASK ? 12 : 8, NP);
         lw_half_read<MASK>(ring, da_lds, h1, dwn, kt + 1, 1, KS, rot);
-        lw_half_mma<MASK>(h0, dwn, acc, 0, d);
-        OTPU_READS_THEN_MMA(8);
+        lw_half_mma<NP, MASK, ALL1>(h0, dwn, acc, 0, dv);
+        OTPU_READS_UNDER_MMA(8, NP);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) dw[i] = dwn[i];
     }
     ring_barrier_tracked();                              // the walk's end
     __builtin_amdgcn_sched_barrier(0);
-    lw_half_mma<MASK>(h1, dw, acc, 1, d);
+    lw_half_mma<NP, MASK, ALL1>(h1, dw, acc, 1, dv);
 }
-#undef OTPU_READS_THEN_MMA
+#undef OTPU_READS_UNDER_MMA
 
 // C3: a copy for the c3 prefill shape (M 512, N 8192, K 2048, dense rows, RSC scale words), its
 // sizes and strides as constants (the kernel runs once a CU from a cold instruction cache)
@@ -1081,8 +1090,8 @@ __global__ __launch_bounds__(512) void gemm_lw_kernel(GemmArgs a) {
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[0][i][j] = v4i{0, 0, 0, 0};
-            if (single) lw_mma_walk1<false>(sRing, sDaAll, acc[0], dv[0], KS, rot);
-            else lw_mma_walk1<true>(sRing, sDaAll, acc[0], dv[0], KS, rot);
+            if (single) lw_mma_walk_h<1, false>(sRing, sDaAll, acc, dv, KS, rot);
+            else lw_mma_walk_h<1, true>(sRing, sDaAll, acc, dv, KS, rot);
             epilogue(acc[0]);
         } else {
             v4i acc[2][4][4];
