@@ -271,6 +271,28 @@ def summarize(outdir):
             name = r["Name"].split("(")[0]
             print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:10.3f} {float(r['MinNs']) / 1e3:10.3f} "
                   f"{float(r['MaxNs']) / 1e3:10.3f} {float(r['Percentage']):6.2f}  {name[:110]}")
+    # a kernel's runs: consecutive dispatches of it with no other kernel between them (a bench
+    # case's graph replays), runs of 10 or more, so that cases sharing a kernel read apart
+    for path in sorted(glob.glob(os.path.join(outdir, "**", "*kernel_trace.csv"), recursive=True)):
+        with open(path) as f:
+            rows = sorted(csv.DictReader(f), key=lambda r: int(r["Dispatch_Id"]))
+        runs, cur = [], []
+        for r in rows:
+            if cur and r["Kernel_Name"] != cur[-1]["Kernel_Name"]:
+                runs.append(cur)
+                cur = []
+            cur.append(r)
+        if cur:
+            runs.append(cur)
+        runs = [u for u in runs if len(u) >= 10]
+        if not runs:
+            continue
+        print(f"# {os.path.relpath(path, outdir)}: runs of one kernel (10 or more dispatches in a row)")
+        print(f"{'run':>4} {'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10}  kernel")
+        for i, u in enumerate(runs):
+            d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in u]
+            print(f"{i:4d} {len(d):6d} {sum(d) / len(d):10.3f} {min(d):10.3f} {max(d):10.3f}  "
+                  f"{u[0]['Kernel_Name'].split('(')[0][:110]}")
     for path in sorted(glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True)):
         print(f"# {os.path.relpath(path, outdir)}")
         agg = collections.defaultdict(lambda: collections.defaultdict(float))
