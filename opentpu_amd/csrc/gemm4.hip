@@ -18,12 +18,13 @@
 // path.
 //
 // Work layout.  A workgroup of 8 waves owns a 128 x 128 output tile.  Waves 0-3 multiply (64 x 64
-// each, 4 x 4 v_mfma_i32_16x16x64_i8 per 64-deep step and plane); waves 4-7 stream and expand:
-// they issue every direct-to-LDS load (the activation stage, a 3-deep ring; the 4-bit rows of a
-// stage with their scale words and the activation offset words, a 4-deep ring one stage further
-// ahead) and turn the nibbles of the next stage into the two int8 planes (a 16-entry table per
-// 32-group and plane, built with packed 16-bit products and read with v_perm_b32), while the
-// multiplying waves run the current stage's MFMAs.  One workgroup barrier a stage.
+// each, 4 x 4 v_mfma_i32_16x16x64_i8 per 64-deep step and plane); waves 4-7 stream: they issue
+// every direct-to-LDS load (the activation stage, a 3-deep ring; the 4-bit rows of a stage with
+// their scale words and the activation offset words, a 4-deep ring one stage further ahead).
+// Every wave turns the nibbles of the next stage into the two int8 planes, one 32-group a thread
+// (a 16-entry table per 32-group and plane, built with packed 16-bit products and read with
+// v_perm_b32), the multiplying waves behind the current stage's MFMAs.  One workgroup barrier a
+// stage.
 #include "otpu_common.h"
 
 namespace otpu {
