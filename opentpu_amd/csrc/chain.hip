@@ -258,23 +258,24 @@ static int chain_pad() {
 // workgroup a CU.  Checked once per device (the kernel's resources do not change); a device where
 // it does not hold refuses plans and steps instead of running into the waits' time-out.
 static int chain_resident_check(const char* what) {
-    static int cache[64] = {0};                          // 0 unknown, 1 fits, -1 does not
+    static int cache[64] = {0};                          // 0 unknown, else 1 + workgroups a CU
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
         return otpu_fail(OTPU_ENODEV, "%s: no current device", what);
     int v = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
-    int per_cu = 0;
     if (v == 0) {
+        int per_cu = 0;
         const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &per_cu, reinterpret_cast<const void*>(chain_kernel), 256, chain_pad());
         if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "%s: occupancy query: %s", what, hipGetErrorString(e));
-        v = (int64_t)per_cu * otpu_cu_count() >= otpu_cu_count() ? 1 : -1;
+        v = 1 + (per_cu > 0 ? per_cu : 0);
         __atomic_store_n(&cache[dev], v, __ATOMIC_RELAXED);
     }
-    if (v < 0)
+    // (one workgroup a CU: the grid is the CU count)
+    if (v - 1 < 1)
         return otpu_fail(OTPU_ELAUNCH,
                          "%s: the persistent step's %d workgroups cannot all be resident at once on this "
-                         "device (%d a CU); use the launch-per-linear path", what, otpu_cu_count(), per_cu);
+                         "device (%d a CU); use the launch-per-linear path", what, otpu_cu_count(), v - 1);
     return OTPU_OK;
 }
 
