@@ -25,6 +25,8 @@
 // (a 16-entry table per 32-group and plane, built with packed 16-bit products and read with
 // v_perm_b32), the multiplying waves behind the current stage's MFMAs.  One workgroup barrier a
 // stage.
+#include <type_traits>
+
 #include "otpu_common.h"
 
 namespace otpu {
@@ -339,8 +341,10 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         if (lane == 0) sFlag[wid] = bad;
     }
     __syncthreads();
-    const uint32_t dall = sFlag[0] | sFlag[1] | sFlag[2] | sFlag[3];
-    const bool wide = (sFlag[4] | sFlag[5] | sFlag[6] | sFlag[7]) != 0;
+    // (read into scalar registers: the compiler then knows the tile's flags are uniform, and the
+    // tests on them stay scalar branches instead of per-lane ones around each use)
+    const uint32_t dall = __builtin_amdgcn_readfirstlane(sFlag[0] | sFlag[1] | sFlag[2] | sFlag[3]);
+    const bool wide = __builtin_amdgcn_readfirstlane(sFlag[4] | sFlag[5] | sFlag[6] | sFlag[7]) != 0;
     const uint32_t dm = dall & ((1u << (W4 + 1)) - 1);
     const bool over = (dall >> 31) != 0;
     const int np = __builtin_popcount(dm);
@@ -379,7 +383,10 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
             const int R = sR[row];
             const int dw = HI ? (int)(word & 0xFF) : 0;
             const int m = HI ? (int)((word >> (8 + 6 * b)) & 63) : 1;
-            const int mp = dw + d <= W4 ? m << (R - dw) : 0;
+            // (arithmetic, no select: as a select the compiler loaded R only where the group is
+            // live, a branch per lane that split the stage's code; a dropped group's shift is
+            // masked, its multiplier 0)
+            const int mp = (m << ((R - dw) & 31)) & -(int)(dw + d <= W4);
             uint32_t tl[4], th[4];
             group_tables<FMT>(mp, tl, th);
             uint32_t l[8], hv[8];
@@ -438,7 +445,11 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         bar();                                  // the streamers' raw 0
         expand(0, d);
         bar();                                  // stage 0 ready
-        for (int kt = 0; kt < KS; ++kt) {
+        // stage kt's MFMAs, and (EXP) the expansion of stage kt + 1 issued between them: the
+        // wave's VALU work runs in the matrix pipe's shadow (after them, it ran alone while the
+        // streaming wave beside it on the SIMD waited at the barrier)
+        auto mstage = [&](int kt, auto exp_next) {
+            constexpr bool EXP = decltype(exp_next)::value;
             const int8_t* A = ringA + (kt % NA) * ATILE;
             const int8_t* PL = planes + (kt & 1) * 2 * PLANE;
             const uint32_t* daw = reinterpret_cast<const uint32_t*>(ringR + (kt % NR) * RSLOT + RAWB + 512);
@@ -447,6 +458,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) dwd[i] = daw[wm * 64 + i * 16 + (lane & 15)];
             }
+            __builtin_amdgcn_sched_barrier(0);
             // every fragment of the stage read before its MFMAs (per 64-deep step, the reads and
             // the MFMAs behind them ran in series)
             v4i fa[2][4], fl[2][4], fh[2][4];
@@ -456,9 +468,10 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
                 const int gsh = 8 * (c >> 1);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    v4i v = *reinterpret_cast<const v4i*>(A + rof(wm * 64 + i * 16 + (lane & 15), c));
-                    if (!single && ((dwd[i] >> gsh) & 0xFFu) != (uint32_t)d) v = v4i{0, 0, 0, 0};
-                    fa[ks][i] = v;
+                    // (the other planes' groups masked arithmetically: as a select the compiler
+                    // branched per lane around each fragment, splitting the stage's schedule)
+                    const int keep = single || ((dwd[i] >> gsh) & 0xFFu) == (uint32_t)d ? -1 : 0;
+                    fa[ks][i] = *reinterpret_cast<const v4i*>(A + rof(wm * 64 + i * 16 + (lane & 15), c)) & keep;
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -476,9 +489,16 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
                         accl[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[ks][i], fl[ks][j], accl[i][j], 0, 0, 0);
                         if (HI) acch[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[ks][i], fh[ks][j], acch[i][j], 0, 0, 0);
                     }
-            if (kt + 1 < KS) expand(kt + 1, d);  // (raw kt + 1 landed before this stage's barrier)
-            bar();                              // stage kt + 1 ready (or the walk's end)
+            if constexpr (EXP) expand(kt + 1, d);   // (raw kt + 1 landed before this stage's barrier)
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        for (int kt = 0; kt + 1 < KS; ++kt) {
+            mstage(kt, std::true_type{});
+            bar();                              // stage kt + 1 ready
+            __builtin_amdgcn_sched_barrier(0);
         }
+        mstage(KS - 1, std::false_type{});
+        bar();                                  // the walk's end
         dprev = d;
     }
 
