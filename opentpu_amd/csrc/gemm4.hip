@@ -506,8 +506,10 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     // Each wave's two planes of sums go to LDS column-major (the four rows an MFMA lane holds
     // are contiguous: one 16-byte write each), then a rolled loop over the wave's 16 row groups
     // (lane: row 4 s + lane / 16, columns 4 (lane & 15) .. + 3) forms each output and stores 4
-    // columns at once.  acc < 2^47 converts to double exactly, and cvt_f32_f64 rounds it as
-    // i2f does (nearest even).
+    // columns at once.  i2f(acc) without int64 arithmetic: acc = T 2^sh is an integer (every live
+    // term is), and rounding commutes with a power-of-two scale where the result stays normal (a
+    // nonzero integer is at least 1), so i2f(acc) = ldexp(RNE(T), sh): T is exact in double
+    // (|T| < 2^40), cvt_f32_f64 rounds it to nearest even, the ldexp is exact.
     // (full tiles: wave w stores row groups 0-7 of region w, stream wave w + 4 groups 8-15)
     const int region = wid & 3;
     int* Tl = reinterpret_cast<int*>(lds) + region * 2 * 64 * TPS;   // [column][row], TPS apart
@@ -541,9 +543,8 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int o = (4 * q + c) * TPS + r;
-            const int64_t T = (HI ? (int64_t)Th[o] * 256 : 0) + (int64_t)Tl[o];
-            const int64_t acc = sh[c] >= 0 ? T * ((int64_t)1 << sh[c]) : T >> (-sh[c]);
-            y[c] = fmul_f(fmul_f((float)(double)acc, sw[c]), sa);
+            const double T = (HI ? (double)Th[o] * 256.0 : 0.0) + (double)Tl[o];   // exact: |T| < 2^40
+            y[c] = fmul_f(fmul_f(__builtin_ldexpf((float)T, sh[c]), sw[c]), sa);
         }
         float* p = a.out + (int64_t)m * a.ors + nc;
         if (full) {
