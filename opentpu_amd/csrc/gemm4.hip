@@ -534,7 +534,9 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     const bool full = m0 + TM <= a.M && n0 + TN <= a.N && a.vec4;
     const bool asc = (a.flags & OTPU_ASCALE) != 0, accf = (a.flags & OTPU_ACC) != 0;
     const int s0 = streamer ? 8 : 0;
-#pragma unroll 1
+    // (two row groups a trip: their LDS reads and conversion chains overlap; one a trip, each
+    // waited on its reads with two waves a SIMD to hide them)
+#pragma unroll 2
     for (int sgrp = s0; sgrp < s0 + 8; ++sgrp) {
         const int r = 4 * sgrp + (lane >> 4);      // the region's row
         const int m = m0 + wm * 64 + r;
