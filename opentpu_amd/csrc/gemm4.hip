@@ -293,29 +293,33 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         sw[c] = unit ? 1.0f : *reinterpret_cast<const float*>(a.ws + (int64_t)min(nc + c, a.N - 1) * a.srs);
     if (streamer) prologue_issue();
 
-    // ---- the tile's scan: activation offsets (waves 0-3), weight offsets and multipliers (4-7) ----
+    // ---- the tile's scan (waves 0-3): activation offsets, weight offsets and multipliers ----
+    // (all of it on the waves that issue no direct loads: their loads' waits then count their own
+    // loads only.  On the streaming waves the weight scan's waits, which the compiler sets
+    // without counting the direct loads issued before them, waited for every stage in flight.)
     if (!streamer) {
         if (tid < TM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-W4)) : 0.0f;
         // two threads a row, a word of four offsets a load (ldda and da 4-byte aligned), the
         // loads of 8 words in flight at once (one at a time, each waited on, the scan took ~30 us)
         uint32_t dm = 0;
-        const int r = tid & (TM - 1), h = tid >> 7;
-        if (m0 + r < a.M) {
-            const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)(m0 + r) * a.ldda);
+        {
+            const int r = tid & (TM - 1), h = tid >> 7;
+            if (m0 + r < a.M) {
+                const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)(m0 + r) * a.ldda);
 #pragma unroll 8
-            for (int k = h; k < KS; k += 2) {
-                const uint32_t wd = drow[k];
+                for (int k = h; k < KS; k += 2) {
+                    const uint32_t wd = drow[k];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint32_t d = (wd >> (8 * t)) & 0xFFu;
-                    dm |= 1u << (d <= W4 ? d : 31);
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t d = (wd >> (8 * t)) & 0xFFu;
+                        dm |= 1u << (d <= W4 ? d : 31);
+                    }
                 }
             }
         }
-        for (int o = 32; o > 0; o >>= 1) dm |= __shfl_xor(dm, o, 64);
-        if (lane == 0) sFlag[wid] = dm;
-    } else {
-        const int ht = tid - 256, r = ht >> 1, h = ht & 1;
+        // the weight rows: two adjacent threads a row, R (the largest live dw) and whether any
+        // |w''| could pass 32256
+        const int r = tid >> 1, h = tid & 1;
         int R = 0, T = 0;
         if (!plainw) {                          // (rows past N: the last row's, which they stream)
             const uint8_t* srow = a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
@@ -323,12 +327,12 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
             for (int k = h; k < KS; k += 2) {
                 const uint32_t word = *reinterpret_cast<const uint32_t*>(srow + 4 * k);
                 const int dw = (int)(word & 0xFF);
-                if (dw > W4) continue;                                   // dropped for every d
                 int mx = 0;
 #pragma unroll
                 for (int b = 0; b < 4; ++b) mx = max(mx, (int)((word >> (8 + 6 * b)) & 63));
-                R = max(R, dw);
-                T = max(T, mx << (W4 - dw));
+                const bool live = dw <= W4;                              // (dropped for every d)
+                R = max(R, live ? dw : 0);
+                T = max(T, live ? mx << (W4 - dw) : 0);
             }
         }
         R = max(R, __shfl_xor(R, 1, 64));
@@ -336,9 +340,15 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         // the largest |w''| of the row: max over live groups of m 2^(R - dw) * MAGMAX
         const int need = plainw ? MAGMAX : (T >> (W4 - R)) * MAGMAX;
         uint32_t bad = need > 32256 ? 1u : 0u;
-        for (int o = 32; o > 0; o >>= 1) bad |= __shfl_xor(bad, o, 64);
+        for (int o = 32; o > 0; o >>= 1) {
+            dm |= __shfl_xor(dm, o, 64);
+            bad |= __shfl_xor(bad, o, 64);
+        }
         if (h == 0) sR[r] = R;
-        if (lane == 0) sFlag[wid] = bad;
+        if (lane == 0) {
+            sFlag[wid] = dm;
+            sFlag[4 + wid] = bad;
+        }
     }
     __syncthreads();
     // (read into scalar registers: the compiler then knows the tile's flags are uniform, and the
