@@ -299,41 +299,34 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     // without counting the direct loads issued before them, waited for every stage in flight.)
     if (!streamer) {
         if (tid < TM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-W4)) : 0.0f;
-        // two threads a row, a word of four offsets a load (ldda and da 4-byte aligned), the
-        // loads of 8 words in flight at once (one at a time, each waited on, the scan took ~30 us)
-        uint32_t dm = 0;
-        {
-            const int r = tid & (TM - 1), h = tid >> 7;
-            if (m0 + r < a.M) {
-                const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)(m0 + r) * a.ldda);
-#pragma unroll 8
-                for (int k = h; k < KS; k += 2) {
-                    const uint32_t wd = drow[k];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const uint32_t d = (wd >> (8 * t)) & 0xFFu;
-                        dm |= 1u << (d <= W4 ? d : 31);
-                    }
-                }
-            }
-        }
-        // the weight rows: two adjacent threads a row, R (the largest live dw) and whether any
-        // |w''| could pass 32256
+        // two adjacent threads a row of each operand (activation row m0 + r, weight row n0 + r),
+        // a word a load (four activation offsets; a weight block's dw and multipliers), both
+        // rows' loads of 8 words in flight at once (with the two scans one after the other, each
+        // waited for its loads: two round trips, ~2 us each while the start's loads all miss)
         const int r = tid >> 1, h = tid & 1;
-        int R = 0, T = 0;
-        if (!plainw) {                          // (rows past N: the last row's, which they stream)
-            const uint8_t* srow = a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
+        const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)min(m0 + r, a.M - 1) * a.ldda);
+        const uint32_t dmask = m0 + r < a.M ? ~0u : 0u;        // (rows past M offer no offsets)
+        const uint8_t* srow = a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
+        uint32_t dm = 0;
+        int R = 0, T = 0;                       // (rows past N: the last row's, which they stream)
 #pragma unroll 8
-            for (int k = h; k < KS; k += 2) {
-                const uint32_t word = *reinterpret_cast<const uint32_t*>(srow + 4 * k);
-                const int dw = (int)(word & 0xFF);
-                int mx = 0;
+        for (int k = h; k < KS; k += 2) {
+            const uint32_t wd = drow[k];
+            const uint32_t word = plainw ? 0u : *reinterpret_cast<const uint32_t*>(srow + 4 * k);
+            uint32_t bits = 0;
 #pragma unroll
-                for (int b = 0; b < 4; ++b) mx = max(mx, (int)((word >> (8 + 6 * b)) & 63));
-                const bool live = dw <= W4;                              // (dropped for every d)
-                R = max(R, live ? dw : 0);
-                T = max(T, live ? mx << (W4 - dw) : 0);
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t d = (wd >> (8 * t)) & 0xFFu;
+                bits |= 1u << (d <= W4 ? d : 31);
             }
+            dm |= bits & dmask;
+            const int dw = (int)(word & 0xFF);
+            int mx = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) mx = max(mx, (int)((word >> (8 + 6 * b)) & 63));
+            const bool live = dw <= W4;                                  // (dropped for every d)
+            R = max(R, live ? dw : 0);
+            T = max(T, live ? mx << (W4 - dw) : 0);
         }
         R = max(R, __shfl_xor(R, 1, 64));
         T = max(T, __shfl_xor(T, 1, 64));
