@@ -277,10 +277,22 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     };
     // the expansion of raw stage s into plane buffer s & 1 for activation plane d (streaming thread
     // (row r, half h): the row's 64 elements of its half, two 32-groups)
-    auto prologue_issue = [&] {                 // raw 0, then (A 0, raw 1), (A 1, raw 2)
+    // a walk's first loads: raw 0, then (A 0, raw 1), (A 1, raw 2), the waits below count them in
+    // that order.  The first walk issues raw 0 and A 0 before the tile's scan and the rest after
+    // it: at the start every CU's loads miss in L2 at once, and the fewer there are, the sooner
+    // the scan's and stage 0's come back.
+    auto prologue_first = [&] {
         issue_r(0);
-        if (KS > 1) { issue_a(0); issue_r(1); } else { issue_a(0); }
-        if (KS > 2) { issue_a(1); issue_r(2); } else if (KS > 1) { issue_a(1); }
+        issue_a(0);
+    };
+    auto prologue_rest = [&] {
+        if (KS > 1) issue_r(1);
+        if (KS > 1) issue_a(1);
+        if (KS > 2) issue_r(2);
+    };
+    auto prologue_issue = [&] {
+        prologue_first();
+        prologue_rest();
     };
     // the epilogue's column scales (region wid & 3's columns), loaded before any stream (a stream
     // wave's waits count only the loads issued after them)
@@ -291,7 +303,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c)
         sw[c] = unit ? 1.0f : *reinterpret_cast<const float*>(a.ws + (int64_t)min(nc + c, a.N - 1) * a.srs);
-    if (streamer) prologue_issue();
+    if (streamer) prologue_first();
 
     // ---- the tile's scan (waves 0-3): activation offsets, weight offsets and multipliers ----
     // (all of it on the waves that issue no direct loads: their loads' waits then count their own
@@ -409,7 +421,8 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     if (streamer) {
         for (uint32_t left = dm; left; left &= left - 1) {     // the activation planes in ascending d
             const int d = __builtin_ctz(left);
-            if (left != dm) prologue_issue();   // (the first plane's: before the scan)
+            if (left != dm) prologue_issue();
+            else prologue_rest();               // (the first plane's first loads: before the scan)
             // raw 0 landed: younger than it the (A 0, raw 1) and (A 1, raw 2) issued
             wait_n((KS > 1 ? DMA_A + DMA_R : DMA_A) + (KS > 2 ? DMA_A + DMA_R : (KS > 1 ? DMA_A : 0)));
             bar();                              // every stream wave's raw 0 (and the planes' last reads)
