@@ -171,10 +171,12 @@ def lm_head(steps, warmup):
     return ms, int(tok.item()), ms_pick, ms_both, sample
 
 
-def gemm(steps, warmup, row_mode=True, fmt="int8"):
+def gemm(steps, warmup, row_mode=True, fmt="int8", generic=False):
     """The c3 prefill GEMM, RSC weights (fmt int8) or 4-bit group-quantized ones (int4x / fp4x6:
     the 4-bit GEMM); activations ROW-quantized (the headline: one scale a row, a single exact
-    plane) or MX (group offsets: several planes)."""
+    plane) or MX (group offsets: several planes).  generic: the output rows padded by 4 floats,
+    so that the int8 GEMM runs its generic copy instead of the one compiled for c3's sizes and
+    strides (the same work)."""
     import torch
 
     from opentpu_amd import _lib as X
@@ -186,14 +188,28 @@ def gemm(steps, warmup, row_mode=True, fmt="int8"):
     fl = X.RSC if fmt == "int8" else 0
     x = torch.randn((M, K), generator=gen, device="cuda")
     q, Sa, da = fp32.quantize_mx(x, 32, row_mode=row_mode)
-    out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    ors = N + 4 if generic else N
+    obuf = torch.empty((M, ors), dtype=torch.float32, device="cuda")
+    out = obuf[:, :N]
 
     def step():
         X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, M, K, X.ptr(rows), rows.shape[1], X.ptr(srows),
-               srows.shape[1], N, X.FMT[fmt], fl, 0, None, X.ptr(out), N, None, X.stream())
+               srows.shape[1], N, X.FMT[fmt], fl, 0, None, X.ptr(out), ors, None, X.stream())
     ms = timed(step, steps, warmup, torch.cuda.current_stream())
-    sample = tuple(t.cpu().numpy() for t in (q, Sa, da, rows, srows, out))
+    sample = tuple(t.cpu().numpy() for t in (q, Sa, da, rows, srows, out.contiguous()))
     return ms, sample
+
+
+def int_mm(steps, warmup):
+    """Yardstick: torch._int_mm (hipBLASLt) at the c3 shape, int8 x int8 -> int32 (the same
+    17.2 G ops; an int32 output of the same 16.8 MB, no MM semantics)."""
+    import torch
+    M, K, N = 512, 2048, 8192
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    A = torch.randint(-127, 128, (M, K), generator=gen, device="cuda", dtype=torch.int8)
+    Bw = torch.randint(-127, 128, (N, K), generator=gen, device="cuda", dtype=torch.int8)   # weight rows, as MM's
+    C = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    return timed(lambda: torch._int_mm(A, Bw.t(), out=C), steps, warmup, torch.cuda.current_stream())
 
 
 def c4_step(steps, warmup, persistent=True):
@@ -434,8 +450,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=80)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c3r,c3m,c3q,c4,c5,copy (default: c1,c2s,c3,c4,"
-                    "c5; c3r / c3m: the ROW / the MX int8 GEMM alone; c3q: the 4-bit GEMMs alone); "
+    ap.add_argument("--only", default="", help="comma list of c1,c2s,c3,c3r,c3m,c3q,c3g,c3blas,c4,c5,copy (default: "
+                    "c1,c2s,c3,c4,c5; c3r / c3m: the ROW / the MX int8 GEMM alone; c3q: the 4-bit GEMMs alone; c3g: "
+                    "the ROW GEMM's generic copy; c3blas: hipBLASLt's int8 GEMM at c3's shape, a yardstick); "
                     "the headline c2 always runs, c2s adds its single-launch figure")
     ap.add_argument("--summarize", metavar="DIR", help="print a text summary of rocprofv3 CSV output and exit")
     args = ap.parse_args()
@@ -510,6 +527,19 @@ def main():
         msf = timed(lambda: o3.fill_(1.0), 20, 2, torch.cuda.current_stream())
         del o3
         extra["c3_output_write_alone"] = {"us": round(msf * 1e3, 2), "what": "torch fill_ of the 512 x 8192 fp32 output"}
+    if "c3" in only or "c3g" in only:
+        # the same ROW GEMM through the generic copy (every shape that is not c3's runs it)
+        ms3g, _ = gemm(20, 2, generic=True)
+        tops = 2 * 512 * 2048 * 8192 / (ms3g * 1e-3) / 1e12
+        extra["c3_gemm_row_x_rsc_generic_copy"] = {"us": round(ms3g * 1e3, 2), "TOPS": round(tops, 2),
+                                                   "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        print(f"[c3 generic copy] {extra['c3_gemm_row_x_rsc_generic_copy']}", file=sys.stderr, flush=True)
+    if "c3blas" in only:
+        msb = int_mm(20, 2)
+        tops = 2 * 512 * 2048 * 8192 / (msb * 1e-3) / 1e12
+        extra["c3_hipblaslt_int_mm"] = {"us": round(msb * 1e3, 2), "TOPS": round(tops, 2),
+                                        "what": "torch._int_mm at 512 x 2048 x 8192, int32 output"}
+        print(f"[c3 hipBLASLt] {extra['c3_hipblaslt_int_mm']}", file=sys.stderr, flush=True)
     if "c3" in only or "c3m" in only:
         ms3m, _ = gemm(20, 2, row_mode=False)
         tops = 2 * 512 * 2048 * 8192 / (ms3m * 1e-3) / 1e12
