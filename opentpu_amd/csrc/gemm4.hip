@@ -275,8 +275,6 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
             default: wait_vm<0>(); break;
         }
     };
-    // the expansion of raw stage s into plane buffer s & 1 for activation plane d (streaming thread
-    // (row r, half h): the row's 64 elements of its half, two 32-groups)
     // a walk's first loads: raw 0, then (A 0, raw 1), (A 1, raw 2), the waits below count them in
     // that order.  The first walk issues raw 0 and A 0 before the tile's scan and the rest after
     // it: at the start every CU's loads miss in L2 at once, and the fewer there are, the sooner
@@ -370,7 +368,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 
     if (dm == 0 || !fits || wide) {
         // every group drops (acc 0), or the exact VALU path
-        if (streamer) wait_vm<0>();             // (the first walk's loads, issued before the scan)
+        if (streamer) wait_vm<0>();             // (the first walk's first loads, issued before the scan)
         for (int idx = tid; idx < TM * TN; idx += 512) {
             const int r = idx / TN, c = idx % TN, m = m0 + r, n = n0 + c;
             if (m >= a.M || n >= a.N) continue;
@@ -381,12 +379,11 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         return;
     }
 
-    // (the two groups in a rolled loop: the kernel runs once a CU from a cold instruction cache,
-    // so the code's length is part of its latency)
-    // Every thread of the workgroup expands one of the stage's 512 32-groups, gi = its thread
-    // index (row gi / 4, the row's group gi % 4): the multiplying waves do theirs behind their
-    // MFMAs, whose matrix pipe runs beside the VALU (the streaming waves alone, two groups a
-    // thread, took ~1.4 us a stage, latency-bound).  A read instruction reads 1 KB of raw nibbles
+    // The expansion of raw stage s into plane buffer s & 1 for activation plane d.  Every thread
+    // of the workgroup expands one of the stage's 512 32-groups, gi = its thread index (row
+    // gi / 4, the row's group gi % 4): the multiplying waves do theirs between their MFMAs,
+    // whose matrix pipe runs beside the VALU (the streaming waves alone, two groups a thread,
+    // took ~1.4 us a stage, latency-bound).  A read instruction reads 1 KB of raw nibbles
     // contiguously, free of bank conflicts.
     auto expand = [&](int s, int d) {
         const int8_t* slot = ringR + (s % NR) * RSLOT;
