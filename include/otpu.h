@@ -60,7 +60,7 @@ enum {
 /* The ABI's version: otpu_version() returns OTPU_ABI_VERSION of the header the library was built
  * with.  It changes whenever an entry point's signature or an operand's size changes, so a caller
  * built against another header can refuse the library (opentpu_amd/_lib.py does). */
-#define OTPU_ABI_VERSION 2
+#define OTPU_ABI_VERSION 3
 
 const char* otpu_last_error(void);
 int otpu_version(void);
@@ -155,14 +155,15 @@ int otpu_mm_qin(const float* x, const float* xmul, const float* rscale, const fl
 /* The chained layer's down projection folded in one launch (Builder.dot's per-range MMs with
  * their ACC, opentpu/compiler.py:2686-2720; swiglu_down's chunk loop,
  * opentpu/kernels/mlp.py:87-120): the fp32 row mul(x, xmul) (xmul may be NULL; then RSCALE and
- * CSCALE as otpu_mm_qin, either may be NULL) in K / 256 ranges of 256 columns (the 4-bit down chunk at F = 3072, opentpu/kernels/mlp.py:8-24), each
- * quantized by its own QACT and multiplied by its weight columns, and the ranges' outputs added
- * in range order into out[0..N): otpu_mm_qin's ranges and the fold of their rows, bit for bit.
- * 4-bit weights with scale rows only (INT4, FP4, NVFP4; no flags but PAIR); K a multiple of 256,
- * at most 4096. */
+ * CSCALE as otpu_mm_qin, either may be NULL) in K / width ranges of width columns (the 4-bit down
+ * chunk, opentpu/kernels/mlp.py:8-30: 256 at F = 3072, 768 at F = 6144), each quantized by its
+ * own QACT and multiplied by its weight columns, and the ranges' outputs added in range order into
+ * out[0..N): otpu_mm_qin's ranges and the fold of their rows, bit for bit.  4-bit weights with
+ * scale rows only (INT4, FP4, NVFP4; no flags but PAIR); K a multiple of 256, at most 8192; width
+ * a multiple of 256 that divides K. */
 int otpu_mm_qin_fold(const float* x, const float* xmul, const float* rscale, const float* cscale, int K,
-                     const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
-                     int k0, float* out, otpu_stream_t stream);
+                     int width, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt,
+                     int flags, int k0, float* out, otpu_stream_t stream);
 
 /* MM SPL (split terms: opentpu/isasim.py:757-770, :849-852, :872-873; docs/isa.md:414-441): one
  * MM over a split operand's terms, one K-block (128) of int8 RSC weights a part, natural rows.
@@ -195,8 +196,11 @@ int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float
  *   the order qkv, o, gu, down (each layer's strides equal layer 0's); rnorm: RSCALE factors
  *   [layers, 2] (device) or NULL; cscale: 2 a layer (gamma of the qkv and the gate/up QACTs,
  *   device, entries may be NULL) or NULL; x: the step's input row [hidden]; outs: the phases' fp32
- *   output rows (qkv [q_dim + 2 kv_dim], o [hidden], gu [2 F], down [hidden]).  int4x or fp4x6
- *   weights; hidden <= 1024, q_dim <= 2048, F a multiple of 256 and <= 4096, hidden and q_dim
+ *   output rows (qkv [q_dim + 2 kv_dim], o [hidden], gu [2 F], down [hidden]); down_width: the
+ *   down projection's QACT range (a multiple of 256 dividing F; the reference's chunk rule gives
+ *   256 at F = 3072, 768 at F = 6144).  int4x or fp4x6 weights; hidden <= 2048, q_dim <= 2048, F
+ *   a multiple of 256 and <= 8192 (hidden <= 1024 and F <= 4096, Qwen3-0.6B's sizes, run teams of
+ *   one and two pieces a lane, larger shapes up to Qwen3-1.7B's two and four), hidden and q_dim
  *   multiples of 32.
  *   otpu_chain_step: one step (reads x, writes every output row); capturable in a HIP graph.
  *   Steps on one plan must not overlap (issue them on one stream).  A step needs all of its
@@ -207,10 +211,10 @@ int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float
  *   polls, the outputs since are invalid), synchronous.  It stays set until the plan is
  *   written again. */
 int64_t otpu_chain_plan_bytes(int layers, int hidden, int q_dim, int kv_dim, int F);
-int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int fmt, const uint8_t* const* w,
-                    const int64_t* rs, const uint8_t* const* ws, const int64_t* srs, const float* rnorm,
-                    const float* const* cscale, const float* x, float* const* outs, void* plan,
-                    int64_t plan_bytes);
+int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int down_width, int fmt,
+                    const uint8_t* const* w, const int64_t* rs, const uint8_t* const* ws, const int64_t* srs,
+                    const float* rnorm, const float* const* cscale, const float* x, float* const* outs,
+                    void* plan, int64_t plan_bytes);
 int otpu_chain_step(const void* plan, otpu_stream_t stream);
 int otpu_chain_error(const void* plan, uint32_t* err);
 /* Profiling: clock stamps of every phase and workgroup into stamps [4 layers][grid][8] (uint64,

@@ -19,7 +19,7 @@ UNIT, ACC, RMAX, ASCALE, PAIR, RSC = 0x1, 0x2, 0x4, 0x8, 0x40, 0x80
 Q_ROW, Q_LO, Q_HL = 0x1, 0x10, 0x20             # QACT / QST flags
 QALIGN = 64                                     # QACT ST / LDA row alignment
 LM_STATE_BYTES = 16640                          # the LM head's state (result word, maxima)
-ABI_VERSION = 2                                 # include/otpu.h OTPU_ABI_VERSION this binding follows
+ABI_VERSION = 3                                 # include/otpu.h OTPU_ABI_VERSION this binding follows
 
 # every exported symbol and its argument types (P pointer, L int64, I int32, F float, D double)
 _P, _L, _I, _F, _D = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double
@@ -40,11 +40,11 @@ SIGNATURES = {
     "otpu_mm_ranges": ([_P, _L, _P, _P, _L, _I, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P], _I),
     "otpu_vmul": ([_P, _P, _P, _L, _P], _I),
     "otpu_mm_qin": ([_P, _P, _P, _P, _I, _L, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _L, _P], _I),
-    "otpu_mm_qin_fold": ([_P, _P, _P, _P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P], _I),
+    "otpu_mm_qin_fold": ([_P, _P, _P, _P, _I, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _P], _I),
     "otpu_mm_spl": ([_P, _L, _P, _P, _L, _I, _I, _P, _L, _L, _P, _L, _I, _I, _P, _L, _P], _I),
     "otpu_acc_rows": ([_P, _I, _L, _I, _P, _P, _P], _I),
     "otpu_chain_plan_bytes": ([_I, _I, _I, _I, _I], _L),
-    "otpu_chain_plan": ([_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L], _I),
+    "otpu_chain_plan": ([_I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L], _I),
     "otpu_chain_step": ([_P, _P], _I),
     "otpu_chain_error": ([_P, _P], _I),
     "otpu_chain_stamps": ([_P, _P], _I),

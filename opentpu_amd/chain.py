@@ -61,8 +61,8 @@ class Shape:
 class DecodeChain:
     """`layers`: per layer a dict name -> (rows, srows) device tensors (uint8).
 
-    persistent (default where it applies: fused and folded, int4 / fp4 weights, hidden <= 1024,
-    q_dim <= 2048, F <= 4096): the whole step is one launch of otpu_chain_step, its phases handing
+    persistent (default where it applies: fused and folded, int4 / fp4 weights, hidden <= 2048,
+    q_dim <= 2048, F <= 8192): the whole step is one launch of otpu_chain_step, its phases handing
     rows to each other on the GPU; the same bits as the four kernels a layer below.
     fused: a layer is four kernels, each linear an otpu_mm_qin (the QACT of its input
     row in the GEMV's prologue).  With 4-bit weights and 256-column down chunks the down
@@ -89,7 +89,7 @@ class DecodeChain:
         self.R = s.F // self.width
         # the down projection folded in its own launch (4-bit, 256-column chunks); False keeps
         # the per-chunk partial rows folded by the next layer's prologue
-        self.fold = fmt != "int8" and self.width == 256 and s.F <= 4096
+        self.fold = fmt != "int8" and self.width % 256 == 0 and s.F <= 8192
         nq = s.q_dim + 2 * s.kv_dim
         T = X.torch()
         dev = "cuda"
@@ -118,7 +118,7 @@ class DecodeChain:
         self.persistent = self.persistent_fits() if persistent is None else bool(persistent)
         if self.persistent and not self.persistent_fits():
             raise ValueError("DecodeChain: the persistent step needs fused, folded int4 / fp4 layers with "
-                             "hidden <= 1024, q_dim <= 2048, F <= 4096 (and 2 kv_dim <= 2048 where o "
+                             "hidden <= 2048, q_dim <= 2048, F <= 8192 (and 2 kv_dim <= 2048 where o "
                              "waits for k and v)")
 
     @staticmethod
@@ -211,9 +211,9 @@ class DecodeChain:
         self._qin(w["o"], self.qkv, s.q_dim, s.q_dim, self.o)
         self._qin(w["gu"], self.o, s.hidden, s.hidden, self.gu, norm=self._norm(l, 1))
         rows, srows = w["down"]
-        X.call("otpu_mm_qin_fold", X.ptr(self.gu), X.ptr(self.gu[:, s.F:]), None, None, s.F, X.ptr(rows),
-               rows.shape[1], X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0, X.ptr(y),
-               X.stream())
+        X.call("otpu_mm_qin_fold", X.ptr(self.gu), X.ptr(self.gu[:, s.F:]), None, None, s.F, self.width,
+               X.ptr(rows), rows.shape[1], X.ptr(srows), srows.shape[1], rows.shape[0], X.FMT[self.fmt], 0, 0,
+               X.ptr(y), X.stream())
 
     # --- the persistent step ---------------------------------------------------------------
     def persistent_fits(self) -> bool:
@@ -222,8 +222,8 @@ class DecodeChain:
         # o waits for k and v as well when the q/k/v rows (32 a workgroup) span more workgroups
         # than o's (4 a workgroup); that wait holds 2048 entries
         kv_wait = -(-(s.q_dim + 2 * s.kv_dim) // 32) > -(-s.hidden // 4)
-        return (self.fused and self.fold and self.fmt in ("int4", "fp4") and s.hidden <= 1024 and s.hidden % 32 == 0
-                and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 4096 and s.F % 256 == 0
+        return (self.fused and self.fold and self.fmt in ("int4", "fp4") and s.hidden <= 2048 and s.hidden % 32 == 0
+                and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 8192 and s.F % 256 == 0
                 and not (kv_wait and 2 * s.kv_dim > 2048))
 
     def _use_persistent(self) -> bool:
@@ -256,7 +256,7 @@ class DecodeChain:
                 rs[j], srs[j] = rows.shape[1], srows.shape[1]
             if cs is not None:
                 cs[2 * l], cs[2 * l + 1] = X.ptr(self.norms[l][0]), X.ptr(self.norms[l][1])
-        X.call("otpu_chain_plan", n, s.hidden, s.q_dim, s.kv_dim, s.F, X.FMT[self.fmt], w, rs, ws, srs,
+        X.call("otpu_chain_plan", n, s.hidden, s.q_dim, s.kv_dim, s.F, self.width, X.FMT[self.fmt], w, rs, ws, srs,
                X.ptr(self.rnorm) if self.norms is not None else None, cs, X.ptr(self.x), outs, ptr, nbytes)
         self._plan = (buf, ptr)
         return ptr

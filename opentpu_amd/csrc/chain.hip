@@ -38,8 +38,8 @@ int qin_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float
              int nsum, int64_t sum_stride, int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws,
              int64_t srs, int N, int fmt, int flags, int k0, float* out, int64_t ors, int64_t part_stride);
 int fold_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float* rscale, const float* cscale,
-              int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
-              float* out);
+              int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
+              int k0, float* out);
 
 constexpr int CHAIN_SLOTS = 4096;               // workgroups' call counters a plan holds
 constexpr int CHAIN_SPIN = 1 << 16;             // polls a wait allows (~1 us each; OTPU_CHAIN_SPIN at plan time)
@@ -81,6 +81,7 @@ struct ChainPlan {                               // device memory: the header, t
     int kv_wait;                                 // o waits for the k and v entries as well
     int norms;                                   // 0 no RSCALE / CSCALE factors, 1 some, 2 both in every layer
     int spin;                                    // polls a wait allows
+    int combo;                                   // the phases' pieces a lane: 0 (LQ, LO, LF) = (1, 1, 2), 1 (2, 1, 4)
     uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
 };
 
@@ -117,8 +118,10 @@ __device__ __forceinline__ T cload(const T& r) {
 }
 
 // NORMS: 0 no RSCALE / CSCALE factors (constant NULLs), 1 some, 2 both in every layer (the
-// prologues' tests of the factors drop out)
-template <int FMT, bool FIXED, bool C4, int NORMS>
+// prologues' tests of the factors drop out).  LQ, LO, LF: the 16-byte pieces a lane holds in
+// the q/k/v and gate/up phases (32 lanes a row: hidden <= 1024 LQ), in o (64 lanes: q_dim <=
+// 2048 LO) and in the fold (64 lanes: F <= 2048 LF)
+template <int FMT, bool FIXED, bool C4, int NORMS, int LQ = 1, int LO = 1, int LF = DN_L>
 __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     constexpr int NRM = NORMS == 0 ? 1 : NORMS == 2 ? 2 : 0;    // the prologues' factor flag
     const int b = blockIdx.x;
@@ -172,26 +175,26 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             if (k == 1) {
                 if (cload(P.kv_wait)) a.ll_all = cload(P.kind[0].N);   // o waits for k and v too
                 if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; a.rs = 1024; a.srs = 72; }
-                gemv_body<FMT, 1, 1, O_T, false, true, O_R, true, true, 1>(a, &lds.q);
+                gemv_body<FMT, 1, LO, O_T, false, true, O_R, true, true, 1>(a, &lds.q);
             } else if (k == 3) {
-                if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; a.rs = 1536; a.srs = 104; }
+                if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; a.rs = 1536; a.srs = 104; a.fold_c = 1; }
                 // the next layer's table line read into the scalar cache during the fold, so that
                 // its first phase finds its weight pointers there (the empty asm keeps the load;
                 // its wait falls after the fold's own waits): ~1.5 us a step
                 const uint8_t* const next = cload(LY[l + 1 < NL ? l + 1 : l].w[0]);
-                fold_body<FMT, DN_L, DN_T, true>(a, &lds.f);
+                fold_body<FMT, LF, DN_T, true>(a, &lds.f);
                 asm volatile("" ::"s"(next));
             } else if (C4 && k == 0) {                   // (its own call site: its constants)
                 if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 4096; a.gu_pair = 0; a.rs = 512; a.srs = 40; }
-                if (i == 0) gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, false, NRM>(a, &lds.q);   // plain x0
-                else gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
+                if (i == 0) gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, false, NRM>(a, &lds.q);   // plain x0
+                else gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
             } else if (k == 2) {
                 if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 6144; a.gu_pair = 3072; a.rs = 512; a.srs = 40; }
-                gemv_body<FMT, 1, 1, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
+                gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
             } else if (i == 0) {                         // the step's first phase reads the plain x0
-                gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true, false, NRM>(a, &lds.q);
+                gemv_body<FMT, 1, LQ, QKV_T, false, true, QKV_R, true, false, NRM>(a, &lds.q);
             } else {
-                gemv_body<FMT, 1, 1, QKV_T, false, true, QKV_R, true, true, NRM>(a, &lds.q);
+                gemv_body<FMT, 1, LQ, QKV_T, false, true, QKV_R, true, true, NRM>(a, &lds.q);
             }
             OTPU_STAMP(a, 4);
             __syncthreads();                             // the next phase reuses the LDS
@@ -204,10 +207,20 @@ __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
     __shared__ __align__(16) ChainLds lds;
     const ChainPlan& P = *plan;
     const bool fixed = P.spin == CHAIN_SPIN;
-    const bool c4 = OTPU_CHAIN_C4 && fixed && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 &&
-                    P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && !P.kv_wait &&
+    const bool c4 = OTPU_CHAIN_C4 && fixed && P.combo == 0 && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 &&
+                    P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && P.kind[3].fold_c == 1 && !P.kv_wait &&
                     P.kind[0].rs == 512 && P.kind[0].srs == 40 && P.kind[1].rs == 1024 && P.kind[1].srs == 72 &&
                     P.kind[2].rs == 512 && P.kind[2].srs == 40 && P.kind[3].rs == 1536 && P.kind[3].srs == 104;
+    if (P.combo == 1) {                          // hidden <= 2048, q_dim <= 2048, F <= 8192
+        if (P.fmt == OTPU_INT4) {
+            if (fixed) chain_run<OTPU_INT4, true, false, 1, 2, 1, 4>(P, lds);
+            else chain_run<OTPU_INT4, false, false, 1, 2, 1, 4>(P, lds);
+        } else {
+            if (fixed) chain_run<OTPU_FP4, true, false, 1, 2, 1, 4>(P, lds);
+            else chain_run<OTPU_FP4, false, false, 1, 2, 1, 4>(P, lds);
+        }
+        return;
+    }
     if (P.fmt == OTPU_INT4) {
         if (c4 && P.norms == 0) chain_run<OTPU_INT4, true, true, 0>(P, lds);
         else if (c4 && P.norms == 2) chain_run<OTPU_INT4, true, true, 2>(P, lds);
@@ -285,17 +298,19 @@ extern "C" int64_t otpu_chain_plan_bytes(int layers, int hidden, int q_dim, int 
     return chain_layout(layers, maxn).total;
 }
 
-extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int fmt,
+extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int down_width, int fmt,
                                const uint8_t* const* w, const int64_t* rs, const uint8_t* const* ws,
                                const int64_t* srs, const float* rnorm, const float* const* cscale, const float* x,
                                float* const* outs, void* plan, int64_t plan_bytes) {
     if (fmt != OTPU_INT4 && fmt != OTPU_FP4) return otpu_fail(OTPU_EINVAL, "chain_plan: int4x or fp4x6 weights");
     if (layers < 1 || !w || !rs || !ws || !srs || !x || !outs || !plan)
         return otpu_fail(OTPU_EINVAL, "chain_plan: layers %d, NULL arrays", layers);
-    if (hidden > 32 * QKV_T || q_dim > 32 * O_T || F % 256 || F > 32 * DN_T * DN_L || q_dim % 32 || hidden % 32 ||
-        kv_dim < 0)
+    // the compiled teams: combo 0 (pieces a lane 1, 1, 2) or 1 (2, 1, 4)
+    const int combo = hidden <= 32 * QKV_T && q_dim <= 32 * O_T && F <= 32 * DN_T * DN_L ? 0
+                      : hidden <= 2 * 32 * QKV_T && q_dim <= 32 * O_T && F <= 4 * 32 * DN_T ? 1 : -1;
+    if (combo < 0 || F % 256 || q_dim % 32 || hidden % 32 || kv_dim < 0)
         return otpu_fail(OTPU_EINVAL, "chain_plan: hidden %d (<= %d), q_dim %d (<= %d), F %d (a multiple of 256, <= %d)",
-                         hidden, 32 * QKV_T, q_dim, 32 * O_T, F, 32 * DN_T * DN_L);
+                         hidden, 2 * 32 * QKV_T, q_dim, 32 * O_T, F, 4 * 32 * DN_T);
     if ((uintptr_t)plan % 256) return otpu_fail(OTPU_EALIGN, "chain_plan: plan 256-byte aligned");
     const int nq = q_dim + 2 * kv_dim;
     const int maxn = std::max(std::max(nq, hidden), 2 * F);
@@ -323,7 +338,8 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
                 rc = qin_args(&a, &L, x, nullptr, rsc, cs, 1, 0, Ks[k], Ks[k], w[j], rs[j], ws[j], srs[j], Ns[k], fmt, 0,
                               0, outs[j], Ns[k], 0);
             else
-                rc = fold_args(&a, &L, x, x, nullptr, nullptr, F, w[j], rs[j], ws[j], srs[j], hidden, fmt, 0, 0, outs[j]);
+                rc = fold_args(&a, &L, x, x, nullptr, nullptr, F, down_width, w[j], rs[j], ws[j], srs[j], hidden, fmt,
+                               0, 0, outs[j]);
             if (rc) return rc;
             if (l > 0 && (rs[j] != rs[k] || srs[j] != srs[k]))
                 return otpu_fail(OTPU_EINVAL, "chain_plan: layer %d phase %d row strides differ from layer 0's", l, k);
@@ -359,6 +375,7 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
     }
     hp.layers = layers;
     hp.fmt = fmt;
+    hp.combo = combo;
     {
         bool any = rnorm != nullptr, all = rnorm != nullptr && cscale != nullptr;
         for (int j = 0; cscale && j < 2 * layers; ++j) {

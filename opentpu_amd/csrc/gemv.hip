@@ -337,12 +337,14 @@ void launch_fold(const MMArgs& a, int fmt, int L, hipStream_t s);   // gemv_fold
 // the checks and the argument block of one otpu_mm_qin_fold (pieces a lane in *L; also the
 // persistent chain's down projections)
 int fold_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const float* rscale, const float* cscale,
-              int K, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
-              float* out) {
+              int K, int width, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
+              int k0, float* out) {
     if (fmt == OTPU_INT8) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: 4-bit weights (F-chunks of 256)");
     if (flags & ~OTPU_PAIR) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: no flags (weights with scale rows)");
-    if (K < 256 || K % 256 || K > QIN_KMAX)
-        return otpu_fail(OTPU_EINVAL, "mm_qin_fold: K %d (a multiple of 256, at most %d)", K, QIN_KMAX);
+    if (K < 256 || K % 256 || K > FOLD_KMAX)
+        return otpu_fail(OTPU_EINVAL, "mm_qin_fold: K %d (a multiple of 256, at most %d)", K, FOLD_KMAX);
+    if (width < 256 || width % 256 || K % width)
+        return otpu_fail(OTPU_EINVAL, "mm_qin_fold: width %d (a multiple of 256 dividing K %d)", width, K);
     if (!x || !out) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: x / out NULL");
     if (!al(x, 16) || (xmul && !al(xmul, 16)) || (cscale && !al(cscale, 16)))
         return otpu_fail(OTPU_EALIGN, "mm_qin_fold: x, xmul and cscale 16-byte aligned");
@@ -355,6 +357,7 @@ int fold_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const floa
     a.xin = x; a.xmul = xmul; a.nsum = 1;
     a.rscale = rscale; a.cscale = cscale;
     a.P = (K / 2) / 16;
+    a.fold_c = width / 256;
     int L = 1;
     pick_team(a.P, &a.T, &L);
     if (L > 4) return otpu_fail(OTPU_EINVAL, "mm_qin_fold: K %d needs %d pieces a lane (at most 4)", K, L);
@@ -365,11 +368,11 @@ int fold_args(MMArgs* ap, int* Lp, const float* x, const float* xmul, const floa
 }  // namespace otpu
 
 extern "C" int otpu_mm_qin_fold(const float* x, const float* xmul, const float* rscale, const float* cscale, int K,
-                                const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags,
-                                int k0, float* out, otpu_stream_t stream) {
+                                int width, const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N,
+                                int fmt, int flags, int k0, float* out, otpu_stream_t stream) {
     MMArgs a;
     int L = 1;
-    const int rc = fold_args(&a, &L, x, xmul, rscale, cscale, K, w, rs, ws, srs, N, fmt, flags, k0, out);
+    const int rc = fold_args(&a, &L, x, xmul, rscale, cscale, K, width, w, rs, ws, srs, N, fmt, flags, k0, out);
     if (rc) return rc;
     launch_fold(a, fmt, L, (hipStream_t)stream);
     return otpu_launch_check("mm_qin_fold");

@@ -54,6 +54,7 @@ struct MMArgs {
     int spin;                      // polls a wait allows (~1 us each)
     int ll_all;                    // entries of the input row to wait for when more than K (see ll_drain)
     int gu_pair;                   // F: gate/up rows taken in g / u pairs, the entries g * u (see gemv_body)
+    int fold_c;                    // the folded down projection: 256-column sub-ranges a QACT range (0: 1)
     uint64_t* stamp;               // the phase's clock stamps (builds with OTPU_PHASE_STAMPS only)
 };
 
@@ -72,6 +73,7 @@ struct MMArgs {
 
 constexpr int QIN_KMAX = 4096;     // columns the persistent chain's and the fold's prologue QACT hold in LDS
 constexpr int QIN_KBIG = 16384;    // columns otpu_mm_qin's prologue QACT holds in LDS (its widest kernels)
+constexpr int FOLD_KMAX = 8192;    // columns (F) the folded down projection's prologue QACT holds in LDS
 constexpr int QIN_NSUM_MAX = 16;   // partial rows the prologue folds
 
 // rows a team takes per iteration: 8 rows' loads in flight per wave for one activation row

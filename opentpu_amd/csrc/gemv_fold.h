@@ -20,7 +20,7 @@ namespace otpu {
 
 constexpr int FOLD_C = 256;                       // elements a range
 constexpr int FOLD_PPR = FOLD_C / 32;             // 16-byte pieces a range
-constexpr int FOLD_NRMAX = QIN_KMAX / FOLD_C;     // ranges a row
+constexpr int FOLD_NRMAX = FOLD_KMAX / FOLD_C;    // ranges a row
 
 // lane 8 g's x of each team of T lanes (g < T / 8), at the team's first lane: DPP row_ror:8
 // moves lane 8 to lane 0 within a row of 16; v_permlane16_swap of (x, x) returns the other row
@@ -53,11 +53,13 @@ __device__ __forceinline__ void gather8(float x, float (&v)[T / 8]) {
     }
 }
 
-// the fold's LDS: the quantized row, its group offsets, the ranges' Sa * 2^-W
+// the fold's LDS: the quantized row, its group offsets, each 256-column sub-range's Sa * 2^-W
+// (its range's), the sub-ranges' maxima (ranges of more than one sub-range)
 struct FoldLds {
-    uint32_t qs[QIN_KMAX / 4];
-    uint8_t ds[QIN_KMAX / 32];
+    uint32_t qs[FOLD_KMAX / 4];
+    uint8_t ds[FOLD_KMAX / 32];
     float sa2s[FOLD_NRMAX];
+    uint32_t smaxs[FOLD_NRMAX];
 };
 
 // LL: a phase of the persistent chain: the input row mul(g, u) from hand-off entries (the gate/up
@@ -77,13 +79,17 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
     uint32_t* qs = S->qs;
     uint8_t* ds = S->ds;
     float* sa2s = S->sa2s;
+    uint32_t* smaxs = S->smaxs;
     // float4 chunks a thread holds at most: K <= 32 L T (only the chunks that can exist are
     // compiled: the code runs once per launch, from a cold instruction cache)
     constexpr int CPT0 = (L * T * 8 + 255) / 256;
-    constexpr int CPT = CPT0 < QIN_KMAX / 4 / 256 ? CPT0 : QIN_KMAX / 4 / 256;
+    constexpr int CPT = CPT0 < FOLD_KMAX / 4 / 256 ? CPT0 : FOLD_KMAX / 4 / 256;
     constexpr int NT = 64 / T;                    // teams a wave
     constexpr int GPT = T / FOLD_PPR;             // ranges a team slot holds
-    const int K = a.K, NC = K >> 2, W = window_of(FMT), P = a.P, NR = K / FOLD_C;
+    // ranges of FC sub-ranges of 256 columns (the reference's down chunk is 256 up to F = 3840,
+    // then wider: opentpu/kernels/mlp.py:8-30); NS sub-ranges, NR ranges
+    const int FC = a.fold_c > 1 ? a.fold_c : 1;
+    const int K = a.K, NC = K >> 2, W = window_of(FMT), P = a.P, NS = K / FOLD_C, NR = NS / FC;
     // (workgroups of 256 threads: the mask tells the compiler so, and the chunk tests below then
     // resolve at compile time where K is a constant)
     const int tid = threadIdx.x & 255, lane = tid & 63, tl = lane & (T - 1), team = lane / T;
@@ -172,8 +178,25 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
                     max(fbits(t.z) & 0x7FFFFFFFu, fbits(t.w) & 0x7FFFFFFFu));
     }
 #pragma unroll
-    for (int k = 0; k < CPT; ++k)                          // the range's maximum, and on the way
+    for (int k = 0; k < CPT; ++k)                          // the sub-range's maximum, and on the way
         am[k] = wave_max_dpp_64_8(cm[k], gm[k]);          // the 8 chunks' of this 32-group
+    if (FC > 1) {                                          // (uniform) a range's maximum over its
+#pragma unroll                                             // sub-ranges, which other waves hold
+        for (int k = 0; k < CPT; ++k) {
+            const int c = tid + 256 * k;
+            if (c < NC && lane == 0) smaxs[c >> 6] = am[k];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const int c = tid + 256 * k;
+            if (c >= NC) continue;                           // whole waves: uniform
+            const int r0 = (c >> 6) / FC * FC;
+            uint32_t m = 0;
+            for (int j = 0; j < FC; ++j) m = max(m, smaxs[r0 + j]);
+            am[k] = m;
+        }
+    }
     // The chunks' quantization without branches (with one wave a SIMD a branch serializes what
     // follows it; branch-free, the chunks' chains interleave): no test of the range maximum
     // (recip(0) is 0, so a zero range quantizes to 0 and its Sa is 0) or of the group maximum
@@ -238,7 +261,7 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
     for (int n0 = wave * NT; n0 < a.N; n0 += nwaves * NT) {
         const int n = n0 + team;
         if (n0 != wave * NT) load(st, n);
-        float yr[L];
+        double sr[L];
 #pragma unroll
         for (int i = 0; i < L; ++i) {
             int c0, c1;
@@ -246,22 +269,51 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
             double s = piece_term<FMT, false>(c0, c1, st.sc[i], shA[i], i * T + tl);
             s = xsum(s, 1);
             s = xsum(s, 2);
-            s = xsum(s, 4);
-            // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw and
-            // the finished Sa * 2^-W need no operand flush
-            yr[i] = fmul_f(fmul_f((float)s, LL ? ftz(st.sw) : st.sw), sa2[i]);
+            sr[i] = xsum(s, 4);                          // the sub-range's exact sum
         }
-        // the team's first lane gathers the ranges' outputs (lanes team T + 8 g of slot i hold
-        // range i GPT + g) and adds them in range order; the outputs are fmul results, flushed
+        // fmul(fmul(i2f(acc), Sw), Sa * 2^-W): the float of an integer, the flushed Sw and the
+        // finished Sa * 2^-W need no operand flush
+        const float swf = LL ? ftz(st.sw) : st.sw;
         float y = 0.0f;
+        if (FC == 1) {
+            // every lane its range's epilogue; the team's first lane gathers the outputs (lanes
+            // team T + 8 g of slot i hold range i GPT + g) and adds them in range order (fmul
+            // results, flushed)
+            float yr[L];
 #pragma unroll
-        for (int i = 0; i < L; ++i) {
-            float v[GPT];
-            gather8<T>(yr[i], v);
+            for (int i = 0; i < L; ++i) yr[i] = fmul_f(fmul_f((float)sr[i], swf), sa2[i]);
 #pragma unroll
-            for (int g = 0; g < GPT; ++g) {
-                const int r = i * GPT + g;
-                if (r < NR) y = r ? fadd_f(y, v[g]) : v[g];
+            for (int i = 0; i < L; ++i) {
+                float v[GPT];
+                gather8<T>(yr[i], v);
+#pragma unroll
+                for (int g = 0; g < GPT; ++g) {
+                    const int r = i * GPT + g;
+                    if (r < NR) y = r ? fadd_f(y, v[g]) : v[g];
+                }
+            }
+        } else {
+            // the team's first lane gathers the sub-ranges' exact sums in order, adds each
+            // range's FC of them (integers below 2^53: exact in double), then the range's
+            // epilogue, and folds the ranges in order
+            double acc = 0.0;
+#pragma unroll
+            for (int i = 0; i < L; ++i) {
+                float vh[GPT], vl[GPT], vs[GPT];
+                gather8<T>(__int_as_float(__double2hiint(sr[i])), vh);
+                gather8<T>(__int_as_float(__double2loint(sr[i])), vl);
+                gather8<T>(sa2[i], vs);
+#pragma unroll
+                for (int g = 0; g < GPT; ++g) {
+                    const int u = i * GPT + g;
+                    if (u >= NS) continue;
+                    acc += __hiloint2double(__float_as_int(vh[g]), __float_as_int(vl[g]));
+                    if ((u + 1) % FC == 0) {
+                        const float yv = fmul_f(fmul_f((float)acc, swf), vs[g]);
+                        y = u + 1 > FC ? fadd_f(y, yv) : yv;
+                        acc = 0.0;
+                    }
+                }
             }
         }
         if (tl == 0 && n < a.N) {

@@ -96,10 +96,11 @@ def layer(x, wts: dict, fmt: str = "int4", q_dim: int = 2048, F_dim: int = 3072,
     return y, {"qkv": qkv, "o": o, "gu": gu, "h": h, "down": y}
 
 
-def step(x, layers: list, fmt: str = "int4", q_dim: int = 2048, F_dim: int = 3072, norms=None):
-    """The decode step: every layer in order; returns the last layer's output."""
+def step(x, layers: list, fmt: str = "int4", q_dim: int = 2048, F_dim: int = 3072, norms=None, mm=MM.mm):
+    """The decode step: every layer in order; returns the last layer's output (mm: the MM
+    oracle, numpy's or the C restatement's)."""
     for i, wts in enumerate(layers):
-        x, _ = layer(x, wts, fmt, q_dim, F_dim, norms[i] if norms is not None else None)
+        x, _ = layer(x, wts, fmt, q_dim, F_dim, norms[i] if norms is not None else None, mm=mm)
     return x
 
 

@@ -9,6 +9,7 @@ import pytest
 
 from conftest import same_bits
 from oracle import chain as CH
+from oracle import cpu as OC
 from oracle import fp32 as F
 from oracle import mm as MM
 
@@ -151,23 +152,28 @@ def test_mm_qin(X, fmt, K, width, nsum, mul):
         assert same_bits(got[r:r + 1], y), f"range {r}"
 
 
-@pytest.mark.parametrize("fmt,K,N", [("int4", 3072, 1024), ("int4", 1024, 300), ("fp4", 1536, 257),
-                                      ("nvfp4", 2048, 130), ("int4", 4096, 77)])
-def test_mm_qin_fold(X, fmt, K, N):
-    """The down projection folded in one launch: QACT of every 256-column range of mul(g, u), an
-    MM per range and the ACC of the ranges in order, against the oracle's ranges_dot."""
+@pytest.mark.parametrize("fmt,K,N,width", [("int4", 3072, 1024, 256), ("int4", 1024, 300, 256),
+                                            ("fp4", 1536, 257, 256), ("nvfp4", 2048, 130, 256),
+                                            ("int4", 4096, 77, 256), ("int4", 4096, 150, 512),
+                                            ("int4", 6144, 200, 768), ("fp4", 8192, 96, 1024),
+                                            ("nvfp4", 6144, 64, 1536), ("int4", 7680, 40, 2560)])
+def test_mm_qin_fold(X, fmt, K, N, width):
+    """The down projection folded in one launch: QACT of every range of width columns of
+    mul(g, u) (256, and the reference's wider chunks: 768 at F = 6144, 1024 at 8192; ranges that
+    straddle a team slot's 256-column sub-ranges), an MM per range and the ACC of the ranges in
+    order, against the oracle's ranges_dot."""
     import torch
     from oracle import formats as Q
     rng = np.random.default_rng(K + N + len(fmt))
     W = (spread(rng, N, K, 1.5, 128) * 0.02).astype(np.float32)
     rows, srows = Q.quantize_mxu(W, fmt)
     g, u = spread(rng, 1, K), spread(rng, 1, K)
-    want = CH.ranges_dot(F.mul(g, u), (rows, srows), fmt, 256)
-    say("mm_qin_fold", fmt, K, N)
+    want = CH.ranges_dot(F.mul(g, u), (rows, srows), fmt, width)
+    say("mm_qin_fold", fmt, K, N, width)
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     gd, ud, wd, sd = d(g), d(u), d(rows), d(srows)
     out = torch.full((1, N), 7.0, dtype=torch.float32, device="cuda")
-    X.call("otpu_mm_qin_fold", X.ptr(gd), X.ptr(ud), None, None, K, X.ptr(wd), rows.shape[1], X.ptr(sd),
+    X.call("otpu_mm_qin_fold", X.ptr(gd), X.ptr(ud), None, None, K, width, X.ptr(wd), rows.shape[1], X.ptr(sd),
            srows.shape[1], N, X.FMT[fmt], 0, 0, X.ptr(out), X.stream())
     assert same_bits(out.cpu().numpy(), want)
 
@@ -175,11 +181,12 @@ def test_mm_qin_fold(X, fmt, K, N):
 def test_mm_qin_fold_refusals(X):
     from opentpu_amd._lib import OtpuError
     p = 256
-    for args in [(1024, X.FMT["int8"], 0), (1000, X.FMT["int4"], 0), (8192, X.FMT["int4"], 0),
-                 (1024, X.FMT["int4"], X.RSC)]:
-        K, fmt, flags = args
+    for args in [(1024, 256, X.FMT["int8"], 0), (1000, 256, X.FMT["int4"], 0), (8448, 256, X.FMT["int4"], 0),
+                 (1024, 256, X.FMT["int4"], X.RSC), (1024, 384, X.FMT["int4"], 0), (1536, 1024, X.FMT["int4"], 0),
+                 (1024, 0, X.FMT["int4"], 0)]:
+        K, width, fmt, flags = args
         with pytest.raises(OtpuError):
-            X.call("otpu_mm_qin_fold", p, p, None, None, K, p, 512, p, 40, 8, fmt, flags, 0, p, X.stream())
+            X.call("otpu_mm_qin_fold", p, p, None, None, K, width, p, 512, p, 40, 8, fmt, flags, 0, p, X.stream())
 
 
 def test_acc_rows(X):
@@ -373,13 +380,16 @@ def test_chain_c4_layers_against_the_float64_emulation(X):
 @pytest.mark.parametrize("fmt,hidden,q_dim,kv_dim,F,layers", [("fp4", 512, 1024, 256, 1536, 4),
                                                             ("int4", 512, 1024, 256, 1536, 4),
                                                             ("int4", 1024, 2048, 512, 3840, 2),
-                                                            ("fp4", 1024, 2048, 1024, 3072, 2)])
+                                                            ("fp4", 1024, 2048, 1024, 3072, 2),
+                                                            ("int4", 2048, 2048, 1024, 6144, 2),
+                                                            ("fp4", 1536, 2048, 512, 8192, 2)])
 def test_chain_persistent_formats_and_shapes(X, fmt, hidden, q_dim, kv_dim, F, layers):
     """The persistent step (otpu_chain_step) on fp4x6 and int4x weights, at a shape whose phases
-    leave most workgroups without rows, at the largest F with 256-column down chunks (3840) and at
-    the Qwen3-0.6B shape in fp4x6 (its shape-specialized copy; int4x is the c4 test's), with
-    per-layer norms: the oracle's step bit for bit, eager and over graph replays with new inputs,
-    the error word 0."""
+    leave most workgroups without rows, at the largest F of the one-piece teams' copy with
+    256-column down chunks (3840), at the Qwen3-0.6B shape in fp4x6 (its shape-specialized copy;
+    int4x is the c4 test's), and in the wider teams' copy at the Qwen3-1.7B shape (hidden 2048,
+    F 6144) and at F 8192 (its largest), with per-layer norms: the oracle's step bit for bit,
+    eager and over graph replays with new inputs, the error word 0."""
     import torch
     from opentpu_amd.chain import DecodeChain, Shape
     sh = Shape(hidden=hidden, q_dim=q_dim, kv_dim=kv_dim, F=F, layers=layers)
@@ -395,7 +405,7 @@ def test_chain_persistent_formats_and_shapes(X, fmt, hidden, q_dim, kv_dim, F, l
     host = _host_layers(ch)
     onorms = [(norms[l][0], norms[l][1], r[l, 0:1], r[l, 1:2]) for l in range(sh.layers)]
     xs = [rng.standard_normal((1, hidden)).astype(np.float32) for _ in range(3)]
-    wants = [CH.step(x, host, fmt, q_dim, F, onorms) for x in xs]
+    wants = [CH.step(x, host, fmt, q_dim, F, onorms, mm=OC.mm) for x in xs]
     assert same_bits(ch.step(xs[0]).cpu().numpy(), wants[0])
     ch.capture()
     for i in range(4):
@@ -415,16 +425,16 @@ def test_chain_plan_refusals(X):
     I4 = C.c_int64 * 4
     p = X.ptr(buf)
     arr = P4(p, p, p, p)
-    for layers, hidden, q, kv, F, fmt in ((1, 2048, 2048, 512, 3072, 1), (1, 1024, 4096, 512, 3072, 1),
+    for layers, hidden, q, kv, F, fmt in ((1, 2304, 2048, 512, 3072, 1), (1, 1024, 4096, 512, 3072, 1),
                                          (1, 1024, 2048, 512, 3200, 1), (1, 1024, 2048, 512, 3072, 0),
-                                         (1, 1024, 2048, 512, 4352, 2), (0, 1024, 2048, 512, 3072, 1)):
+                                         (1, 1024, 2048, 512, 8448, 2), (0, 1024, 2048, 512, 3072, 1)):
         with pytest.raises(OtpuError):
-            X.call("otpu_chain_plan", layers, hidden, q, kv, F, fmt, arr, I4(512, 1024, 512, 1536), arr,
+            X.call("otpu_chain_plan", layers, hidden, q, kv, F, 256, fmt, arr, I4(512, 1024, 512, 1536), arr,
                    I4(64, 128, 64, 192), None, None, p, arr, p, 1 << 20)
     # o waits for k and v when the q/k/v rows span more workgroups than o's (hidden 256: o on 64
     # workgroups, q/k/v on 129); that wait holds 2048 entries
     with pytest.raises(OtpuError, match="kv_dim"):
-        X.call("otpu_chain_plan", 1, 256, 2048, 1040, 768, 1, arr, I4(512, 1024, 512, 1536), arr,
+        X.call("otpu_chain_plan", 1, 256, 2048, 1040, 768, 256, 1, arr, I4(512, 1024, 512, 1536), arr,
                I4(64, 128, 64, 192), None, None, p, arr, p, 1 << 20)
     assert X.load().otpu_chain_plan_bytes(0, 1024, 2048, 512, 3072) == -1
 

@@ -190,7 +190,7 @@ def test_mm_qin_fold_premultiplies(ops, fmt, K, N, rc):
     out = torch.full((1, N), 7.0, dtype=torch.float32, device="cuda")
     say("mm_qin_fold premultiplies", fmt, K, N, rc)
     X.call("otpu_mm_qin_fold", X.ptr(gd), X.ptr(ud), X.ptr(rd) if "r" in rc else None,
-           X.ptr(cd) if "c" in rc else None, K, X.ptr(wd), rows.shape[1], X.ptr(sd), srows.shape[1], N,
+           X.ptr(cd) if "c" in rc else None, K, 256, X.ptr(wd), rows.shape[1], X.ptr(sd), srows.shape[1], N,
            X.FMT[fmt], 0, 0, X.ptr(out), X.stream())
     assert same_bits(out.cpu().numpy(), want)
 
