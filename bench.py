@@ -172,7 +172,7 @@ def lm_head(steps, warmup):
 
 
 def gemm(steps, warmup, row_mode=True, fmt="int8", generic=False):
-    """The c3 prefill GEMM, RSC weights (fmt int8) or 4-bit group-quantized ones (int4x / fp4x6:
+    """The c3 prefill GEMM, RSC weights (fmt int8) or 4-bit group-quantized ones (int4x / fp4x6 / nvfp4:
     the 4-bit GEMM); activations ROW-quantized (the headline: one scale a row, a single exact
     plane) or MX (group offsets: several planes).  generic: the output rows padded by 4 floats,
     so that the int8 GEMM runs its generic copy instead of the one compiled for c3's sizes and
@@ -547,15 +547,16 @@ def main():
                                      "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         print(f"[c3 mx] {extra['c3_gemm_mx_x_rsc']}", file=sys.stderr, flush=True)
     if "c3" in only or "c3q" in only:
-        # the c3 shape with 4-bit group-quantized weights (int4x, fp4x6): the 4-bit GEMM, whose
-        # two weight planes make two int8 MFMA products of the c3 size
-        for f4 in ("int4", "fp4"):
+        # the c3 shape with 4-bit group-quantized weights (int4x, fp4x6, nvfp4): the 4-bit GEMM,
+        # whose two weight planes make two int8 MFMA products of the c3 size
+        for f4 in ("int4", "fp4", "nvfp4"):
             for rm, tag in ((True, "row"), (False, "mx")):
                 ms4, _ = gemm(20, 2, row_mode=rm, fmt=f4)
                 tops = 2 * 512 * 2048 * 8192 / (ms4 * 1e-3) / 1e12
-                extra[f"c3_gemm_{tag}_x_{f4}x"] = {"us": round(ms4 * 1e3, 2), "TOPS": round(tops, 2),
-                                                   "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
-                print(f"[c3 {f4} {tag}] {extra[f'c3_gemm_{tag}_x_{f4}x']}", file=sys.stderr, flush=True)
+                key = f"c3_gemm_{tag}_x_{f4}" + ("" if f4 == "nvfp4" else "x")
+                extra[key] = {"us": round(ms4 * 1e3, 2), "TOPS": round(tops, 2),
+                              "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+                print(f"[c3 {f4} {tag}] {extra[key]}", file=sys.stderr, flush=True)
 
     cpu = None if args.no_cpu else cpu_baseline(samples)
     if cpu is not None:

@@ -1,19 +1,22 @@
-// MM for many activation rows with 4-bit weights (int4x, fp4x6, and their RSC / UNIT forms) on
-// the int8 MFMA units: the prefill GEMM of the 4-bit formats.  Semantics: opentpu/isasim.py:
-// 749-910 (docs/isa.md:226-305): acc = sum over 32-groups of [sh >= 0] m 2^sh c, sh = 11 - dw -
-// da, c the group's integer dot product; y = (i2f(acc) * Sw) * (Sa * 2^-11).
+// MM for many activation rows with 4-bit weights (int4x, fp4x6, nvfp4, and their RSC / UNIT
+// forms) on the int8 MFMA units: the prefill GEMM of the 4-bit formats.  Semantics:
+// opentpu/isasim.py:749-910 (docs/isa.md:226-305): acc = sum over groups of [sh >= 0] m 2^sh c,
+// sh = W - dw - da, c the group's integer dot product; y = (i2f(acc) * Sw) * (Sa * 2^-W).  int4x
+// and fp4x6: W = 11, 32-groups with a multiplier m each and a block offset dw per 128 columns;
+// nvfp4: W = 13, 16-groups with an E4M3 scale each, m its significand (8 + mantissa, or the
+// mantissa at E = 0) and dw = 15 - max(E, 1).
 //
 // Exactness.  Every product term is folded into an integer weight before the MFMA.  For weight
-// row n let R_n be the largest block offset dw <= 11 (a block with dw > 11 drops for every
+// row n let R_n be the largest group offset dw <= W (a group with dw > W drops for every
 // activation offset).  For the activation plane d (the 32-groups whose offset is d):
-//     acc_d = 2^(11 - R_n - d) * sum_i q_i w''_i,   w''_i = [dw + d <= 11] m 2^(R_n - dw) w_i,
+//     acc_d = 2^(W - R_n - d) * sum_i q_i w''_i,   w''_i = [dw + d <= W] m 2^(R_n - dw) w_i,
 // an ordinary integer matrix product of int8 activations and the integer w'' (|w''| < 2^15 when
 // the tile's offsets and multipliers allow: checked per tile).  w'' is split into two int8 planes
 // in balanced base 256 (w'' = 256 h + l, l and h in [-128, 127]), each an int8 MFMA operand, so
 // the K walk is a plain two-plane int8 GEMM with no rescaling inside it.  Activation planes (MX
 // offsets) walk K once each, combined by Horner's rule in the int32 accumulators (acc <<= the gap
 // to the next plane's d, as the int8 GEMM does; the bound is checked per tile).  The epilogue
-// forms T = 256 C_h + C_l in int64 and shifts it by 11 - R_n - d_last (exact: the accumulator is
+// forms T = 256 C_h + C_l in int64 and shifts it by W - R_n - d_last (exact: the accumulator is
 // an integer), then the reference's fp32 epilogue.  A tile the bounds refuse takes an exact VALU
 // path.
 //
@@ -22,9 +25,9 @@
 // every direct-to-LDS load (the activation stage, a 3-deep ring; the 4-bit rows of a stage with
 // their scale words and the activation offset words, a 4-deep ring one stage further ahead).
 // Every wave turns the nibbles of the next stage into the two int8 planes, one 32-group a thread
-// (a 16-entry table per 32-group and plane, built with packed 16-bit products and read with
-// v_perm_b32), the multiplying waves behind the current stage's MFMAs.  One workgroup barrier a
-// stage.
+// (a 16-entry table per group of one multiplier and plane, built with packed 16-bit products and
+// read with v_perm_b32), the multiplying waves behind the current stage's MFMAs.  One workgroup
+// barrier a stage.
 #include <type_traits>
 
 #include "otpu_common.h"
@@ -36,19 +39,41 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int TM = 128, TN = 128, BK = 128;      // tile rows and columns, K a stage (one block)
-constexpr int W4 = 11;                          // the 4-bit formats' window
 constexpr int NA = 3;                           // activation stages in their ring
 constexpr int NR = 4;                           // raw weight stages in theirs
 constexpr int ATILE = TM * BK;                  // 16 KB of activations a stage
 constexpr int RAWB = TN * BK / 2;               // 8 KB of nibbles a stage
-constexpr int RSLOT = RAWB + 512 + 512;         // nibbles, scale words, activation offset words
 constexpr int PLANE = TN * BK;                  // one int8 plane of a stage's weights: 16 KB
 constexpr int OFF_RAW = NA * ATILE;
-constexpr int OFF_PL = OFF_RAW + NR * RSLOT;
-constexpr int LDS_BYTES = OFF_PL + 2 * 2 * PLANE;
 constexpr int TPS = 68;                         // the epilogue's transpose row stride (words)
-static_assert(4 * 2 * 64 * TPS * 4 <= LDS_BYTES, "the epilogue's two planes a wave fit the walk's memory");
-static_assert(LDS_BYTES <= 160 * 1024, "one workgroup a CU");
+
+// the formats' constants: MM's window; a raw stage slot's layout (nibbles, then the rows' scale
+// data of the stage: 4 bytes a row, or nvfp4's 8 E4M3 bytes; then the activation rows' offset
+// words; nvfp4 also a pad, below); the direct loads a streaming wave issues a raw stage
+template <int FMT>
+struct Fmt {
+    static constexpr bool NV = FMT == OTPU_NVFP4;
+    static constexpr int W = NV ? 13 : 11;
+    static constexpr int SC = NV ? 1024 : 512;  // scale data of a stage's 128 rows
+    static constexpr int DOFF = RAWB + SC;      // the activation offset words (128 rows)
+    static constexpr int RSLOT = DOFF + 512 + (NV ? 512 : 0);
+    static constexpr int OFF_PL = OFF_RAW + NR * RSLOT;
+    static constexpr int LDS_BYTES = OFF_PL + 2 * 2 * PLANE;
+    static constexpr int DMA_R = NV ? 4 : 3;
+    static constexpr int MAGMAX = FMT == OTPU_INT4 ? 8 : 12;
+    static_assert(4 * 2 * 64 * TPS * 4 <= LDS_BYTES, "the epilogue's two planes a wave fit the walk's memory");
+    static_assert(LDS_BYTES <= 160 * 1024, "one workgroup a CU");
+};
+
+// nvfp4: the multiplier and the offset of an E4M3 group scale (its sign bit unused)
+__device__ __forceinline__ int nv_m(uint32_t e4) {
+    const int E = (int)((e4 >> 3) & 15), mt = (int)(e4 & 7);
+    return E ? 8 + mt : mt;
+}
+__device__ __forceinline__ int nv_dw(uint32_t e4) {
+    const int E = (int)((e4 >> 3) & 15);
+    return 15 - (E > 1 ? E : 1);
+}
 
 struct Args {
     const int8_t* q; int64_t ldq;
@@ -86,9 +111,10 @@ __device__ __forceinline__ void wait_vm() {
 // LDS reads and writes of this wave done, then the workgroup barrier
 __device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
 
-// direct loads a streaming wave issues: per activation stage (16 KB over 4 waves) and per raw
-// stage (8 KB of nibbles over 4 waves, then one dword a lane: scale words or offset words)
-constexpr int DMA_A = 4, DMA_R = 3;
+// direct loads a streaming wave issues per activation stage (16 KB over 4 waves); per raw stage
+// (8 KB of nibbles over 4 waves, then one dword a lane: scale words or offset words; nvfp4 two,
+// below) Fmt::DMA_R
+constexpr int DMA_A = 4;
 
 // ---- the value tables of one 32-group: codes 0..15 times its integer multiplier ----
 // pair k of a format: the values of codes 2k and 2k + 1 (int4 two's complement; fp4x6 twice the
@@ -158,25 +184,33 @@ __device__ __forceinline__ void expand8(uint32_t x, const uint32_t (&tl)[4], con
 template <int FMT>
 __device__ int64_t valu_acc4(const Args& a, int j, int n, bool plainw) {
     constexpr int mag[8] = {0, 1, 2, 3, 4, 6, 8, 12};
+    constexpr int G = Fmt<FMT>::NV ? 2 : 1, GS = 32 / G;     // weight groups a 32-group, their size
     const int8_t* qr = a.q + (int64_t)j * a.ldq;
     const uint8_t* wr = a.w + (int64_t)n * a.rs;
     const uint8_t* srow = a.ws + (int64_t)n * a.srs;
     int64_t acc = 0;
     for (int g = 0; g < a.K / 32; ++g) {
-        int c = 0;
-        for (int i = 0; i < 32; ++i) {
-            const int code = (wr[16 * g + i / 2] >> (4 * (i & 1))) & 15;
-            const int v = FMT == OTPU_INT4 ? (code < 8 ? code : code - 16) : (code & 8 ? -mag[code & 7] : mag[code & 7]);
-            c += (int)qr[32 * g + i] * v;
+        const int da = (int)a.da[(int64_t)j * a.ldda + g];
+        for (int h = 0; h < G; ++h) {
+            int c = 0;
+            for (int i = GS * h; i < GS * (h + 1); ++i) {
+                const int code = (wr[16 * g + i / 2] >> (4 * (i & 1))) & 15;
+                const int v = FMT == OTPU_INT4 ? (code < 8 ? code : code - 16) : (code & 8 ? -mag[code & 7] : mag[code & 7]);
+                c += (int)qr[32 * g + i] * v;
+            }
+            int dw = 0, m = 1;
+            if (!plainw && Fmt<FMT>::NV) {
+                const uint32_t e4 = srow[16 + 8 * (a.k0 + g / 4) + 2 * (g & 3) + h];
+                dw = nv_dw(e4);
+                m = nv_m(e4);
+            } else if (!plainw) {
+                const uint32_t word = *reinterpret_cast<const uint32_t*>(srow + 8 + 4 * (a.k0 + g / 4));
+                dw = (int)(word & 0xFF);
+                m = (int)((word >> (8 + 6 * (g & 3))) & 63);
+            }
+            const int sh = Fmt<FMT>::W - dw - da;
+            if (sh >= 0) acc += ((int64_t)m * c) << sh;
         }
-        int dw = 0, m = 1;
-        if (!plainw) {
-            const uint32_t word = *reinterpret_cast<const uint32_t*>(srow + 8 + 4 * (a.k0 + g / 4));
-            dw = (int)(word & 0xFF);
-            m = (int)((word >> (8 + 6 * (g & 3))) & 63);
-        }
-        const int sh = W4 - dw - (int)a.da[(int64_t)j * a.ldda + g];
-        if (sh >= 0) acc += ((int64_t)m * c) << sh;
     }
     return acc;
 }
@@ -193,9 +227,11 @@ __device__ __forceinline__ void store_out(const Args& a, int m, int n, int64_t a
 // HI: weights with scale rows (two int8 planes); false: RSC / UNIT weights (w'' = w, one plane)
 template <int FMT, bool HI>
 __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
-    __shared__ __align__(16) int8_t lds[LDS_BYTES];
+    using FT = Fmt<FMT>;
+    constexpr int WN = FT::W, RSLOT = FT::RSLOT, DMA_R = FT::DMA_R;
+    __shared__ __align__(16) int8_t lds[FT::LDS_BYTES];
     __shared__ int sR[TN];                      // each weight row's R (the largest live dw)
-    __shared__ float sSa2[TM];                  // the tile rows' Sa * 2^-11
+    __shared__ float sSa2[TM];                  // the tile rows' Sa * 2^-W
     __shared__ uint32_t sFlag[16];              // per wave: d values present, offsets past the window, PL
 
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -217,19 +253,20 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     const bool unit = (a.flags & OTPU_UNIT) != 0;
     const bool plainw = unit || (a.flags & OTPU_RSC) != 0;
     const int KS = a.K / BK;
-    constexpr int MAGMAX = FMT == OTPU_INT4 ? 8 : 12;
+    constexpr int MAGMAX = FT::MAGMAX;
 
     // ---- the streams' sources, and the first walk's first loads (before the scan, whose
     // latency they then overlap) ----
     int8_t* const ringA = lds;
     int8_t* const ringR = lds + OFF_RAW;
-    int8_t* const planes = lds + OFF_PL;        // [buffer][plane][128 x 128]
+    int8_t* const planes = lds + FT::OFF_PL;    // [buffer][plane][128 x 128]
 
     // ---- the streaming waves' sources (per lane) ----
     const int hw = wid & 3;
     const int8_t* srcA[DMA_A];
     const uint8_t* srcB[2];
     const uint8_t* srcW;                        // the dword a lane loads a raw stage (stride per stage below)
+    const uint8_t* srcD = nullptr;              // nvfp4: the second (activation offset words)
     int64_t stepW = 0;
     if (streamer) {
 #pragma unroll
@@ -243,7 +280,16 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
             srcB[u] = a.w + (int64_t)min(n0 + r, a.N - 1) * a.rs + 16 * c;
         }
         const int r = (hw & 1) * 64 + lane;
-        if (hw < 2) {                           // the weight rows' scale words (a dummy for UNIT / RSC)
+        if (FT::NV) {
+            // every wave a quarter of the stage's 8-byte scale rows (dword s = 64 hw + lane: row
+            // s / 2, half s % 2), then the offset words of rows r (waves 2-3 into their area,
+            // waves 0-1 the same words into the pad: every streaming wave issues the same loads)
+            const int sd = hw * 64 + lane;
+            srcW = plainw ? reinterpret_cast<const uint8_t*>(a.q)
+                          : a.ws + (int64_t)min(n0 + (sd >> 1), a.N - 1) * a.srs + 16 + 8 * a.k0 + 4 * (sd & 1);
+            stepW = plainw ? 0 : 8;
+            srcD = a.da + (int64_t)min(m0 + r, a.M - 1) * a.ldda;
+        } else if (hw < 2) {                    // the weight rows' scale words (a dummy for UNIT / RSC)
             srcW = plainw ? reinterpret_cast<const uint8_t*>(a.q)
                           : a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
             stepW = plainw ? 0 : 4;
@@ -262,13 +308,18 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) dma16(srcB[u] + s * (BK / 2), base + (uint32_t)(hw * 2 + u) * 1024u);
         dma4(srcW + s * stepW, base + (uint32_t)RAWB + (uint32_t)hw * 256u);
+        if (FT::NV)
+            dma4(srcD + s * 4, base + (uint32_t)(FT::DOFF + (hw < 2 ? 512 : 0) + (hw & 1) * 256));
     };
-    // vmcnt(n) for the counts a walk can leave outstanding (n a multiple of 3 or 4 up to 14)
+    // vmcnt(n) for the counts a walk can leave outstanding (sums of DMA_A and DMA_R, up to 16)
     auto wait_n = [&](int n) {
         switch (n) {
+            case 16: wait_vm<16>(); break;
             case 14: wait_vm<14>(); break;
+            case 12: wait_vm<12>(); break;
             case 11: wait_vm<11>(); break;
             case 10: wait_vm<10>(); break;
+            case 8: wait_vm<8>(); break;
             case 7: wait_vm<7>(); break;
             case 4: wait_vm<4>(); break;
             case 3: wait_vm<3>(); break;
@@ -308,7 +359,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     // loads only.  On the streaming waves the weight scan's waits, which the compiler sets
     // without counting the direct loads issued before them, waited for every stage in flight.)
     if (!streamer) {
-        if (tid < TM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-W4)) : 0.0f;
+        if (tid < TM) sSa2[tid] = m0 + tid < a.M ? fmul(a.Sa[m0 + tid], pow2f(-WN)) : 0.0f;
         // two adjacent threads a row of each operand (activation row m0 + r, weight row n0 + r),
         // a word a load (four activation offsets; a weight block's dw and multipliers), both
         // rows' loads of 8 words in flight at once (with the two scans one after the other, each
@@ -316,32 +367,45 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         const int r = tid >> 1, h = tid & 1;
         const uint32_t* drow = reinterpret_cast<const uint32_t*>(a.da + (int64_t)min(m0 + r, a.M - 1) * a.ldda);
         const uint32_t dmask = m0 + r < a.M ? ~0u : 0u;        // (rows past M offer no offsets)
-        const uint8_t* srow = a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + 8 + 4 * a.k0;
+        const uint8_t* srow = a.ws + (int64_t)min(n0 + r, a.N - 1) * a.srs + (FT::NV ? 16 + 8 * a.k0 : 8 + 4 * a.k0);
         uint32_t dm = 0;
         int R = 0, T = 0;                       // (rows past N: the last row's, which they stream)
 #pragma unroll 8
         for (int k = h; k < KS; k += 2) {
             const uint32_t wd = drow[k];
-            const uint32_t word = plainw ? 0u : *reinterpret_cast<const uint32_t*>(srow + 4 * k);
             uint32_t bits = 0;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const uint32_t d = (wd >> (8 * t)) & 0xFFu;
-                bits |= 1u << (d <= W4 ? d : 31);
+                bits |= 1u << (d <= WN ? d : 31);
             }
             dm |= bits & dmask;
-            const int dw = (int)(word & 0xFF);
-            int mx = 0;
+            if (FT::NV) {                       // 8 E4M3 group scales a block: each its own dw
+                const uint32_t* sp = reinterpret_cast<const uint32_t*>(srow + 8 * k);   // (4-byte aligned)
+                const uint2 sc = plainw ? make_uint2(0u, 0u) : make_uint2(sp[0], sp[1]);
 #pragma unroll
-            for (int b = 0; b < 4; ++b) mx = max(mx, (int)((word >> (8 + 6 * b)) & 63));
-            const bool live = dw <= W4;                                  // (dropped for every d)
-            R = max(R, live ? dw : 0);
-            T = max(T, live ? mx << (W4 - dw) : 0);
+                for (int g = 0; g < 8; ++g) {
+                    const uint32_t e4 = ((g < 4 ? sc.x : sc.y) >> (8 * (g & 3))) & 0xFFu;
+                    const int dw = nv_dw(e4);
+                    const bool live = !plainw && dw <= WN;
+                    R = max(R, live ? dw : 0);
+                    T = max(T, live ? nv_m(e4) << (WN - dw) : 0);
+                }
+            } else {
+                const uint32_t word = plainw ? 0u : *reinterpret_cast<const uint32_t*>(srow + 4 * k);
+                const int dw = (int)(word & 0xFF);
+                int mx = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) mx = max(mx, (int)((word >> (8 + 6 * b)) & 63));
+                const bool live = dw <= WN;                              // (dropped for every d)
+                R = max(R, live ? dw : 0);
+                T = max(T, live ? mx << (WN - dw) : 0);
+            }
         }
         R = max(R, __shfl_xor(R, 1, 64));
         T = max(T, __shfl_xor(T, 1, 64));
         // the largest |w''| of the row: max over live groups of m 2^(R - dw) * MAGMAX
-        const int need = plainw ? MAGMAX : (T >> (W4 - R)) * MAGMAX;
+        const int need = plainw ? MAGMAX : (T >> (WN - R)) * MAGMAX;
         uint32_t bad = need > 32256 ? 1u : 0u;
         for (int o = 32; o > 0; o >>= 1) {
             dm |= __shfl_xor(dm, o, 64);
@@ -358,7 +422,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
     // tests on them stay scalar branches instead of per-lane ones around each use)
     const uint32_t dall = __builtin_amdgcn_readfirstlane(sFlag[0] | sFlag[1] | sFlag[2] | sFlag[3]);
     const bool wide = __builtin_amdgcn_readfirstlane(sFlag[4] | sFlag[5] | sFlag[6] | sFlag[7]) != 0;
-    const uint32_t dm = dall & ((1u << (W4 + 1)) - 1);
+    const uint32_t dm = dall & ((1u << (WN + 1)) - 1);
     const bool over = (dall >> 31) != 0;
     const int np = __builtin_popcount(dm);
     const int dmin = dm ? __builtin_ctz(dm) : 0, dmax = dm ? 31 - __builtin_clz(dm) : 0;
@@ -391,19 +455,29 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         {
             const int gi = tid, row = gi >> 2, b = gi & 3;
             const uint4 x = *reinterpret_cast<const uint4*>(slot + 16 * gi);
-            const uint32_t word = *reinterpret_cast<const uint32_t*>(slot + RAWB + 4 * row);
             const int R = sR[row];
-            const int dw = HI ? (int)(word & 0xFF) : 0;
-            const int m = HI ? (int)((word >> (8 + 6 * b)) & 63) : 1;
             // (arithmetic, no select: as a select the compiler loaded R only where the group is
             // live, a branch per lane that split the stage's code; a dropped group's shift is
             // masked, its multiplier 0)
-            const int mp = (m << ((R - dw) & 31)) & -(int)(dw + d <= W4);
-            uint32_t tl[4], th[4];
-            group_tables<FMT>(mp, tl, th);
+            auto fold = [&](int m, int dw) { return (m << ((R - dw) & 31)) & -(int)(dw + d <= WN); };
             uint32_t l[8], hv[8];
-            expand8<HI>(x.x, tl, th, l[0], l[1], hv[0], hv[1]);
-            expand8<HI>(x.y, tl, th, l[2], l[3], hv[2], hv[3]);
+            uint32_t tl[4], th[4];
+            if (FT::NV) {
+                // two 16-groups, each with its own E4M3 scale: elements 0-15 (x.x, x.y) and
+                // 16-31 (x.z, x.w); the second table built after the first's last use
+                const uint32_t e2 = *reinterpret_cast<const uint16_t*>(slot + RAWB + 8 * row + 2 * b);
+                group_tables<FMT>(HI ? fold(nv_m(e2 & 0xFFu), nv_dw(e2 & 0xFFu)) : fold(1, 0), tl, th);
+                expand8<HI>(x.x, tl, th, l[0], l[1], hv[0], hv[1]);
+                expand8<HI>(x.y, tl, th, l[2], l[3], hv[2], hv[3]);
+                group_tables<FMT>(HI ? fold(nv_m(e2 >> 8), nv_dw(e2 >> 8)) : fold(1, 0), tl, th);
+            } else {
+                const uint32_t word = *reinterpret_cast<const uint32_t*>(slot + RAWB + 4 * row);
+                const int dw = HI ? (int)(word & 0xFF) : 0;
+                const int m = HI ? (int)((word >> (8 + 6 * b)) & 63) : 1;
+                group_tables<FMT>(fold(m, dw), tl, th);
+                expand8<HI>(x.x, tl, th, l[0], l[1], hv[0], hv[1]);
+                expand8<HI>(x.y, tl, th, l[2], l[3], hv[2], hv[3]);
+            }
             expand8<HI>(x.z, tl, th, l[4], l[5], hv[4], hv[5]);
             expand8<HI>(x.w, tl, th, l[6], l[7], hv[6], hv[7]);
             *reinterpret_cast<uint4*>(pl + rof(row, 2 * b)) = make_uint4(l[0], l[1], l[2], l[3]);
@@ -465,7 +539,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
             constexpr bool EXP = decltype(exp_next)::value;
             const int8_t* A = ringA + (kt % NA) * ATILE;
             const int8_t* PL = planes + (kt & 1) * 2 * PLANE;
-            const uint32_t* daw = reinterpret_cast<const uint32_t*>(ringR + (kt % NR) * RSLOT + RAWB + 512);
+            const uint32_t* daw = reinterpret_cast<const uint32_t*>(ringR + (kt % NR) * RSLOT + FT::DOFF);
             uint32_t dwd[4] = {0u, 0u, 0u, 0u};
             if (!single) {
 #pragma unroll
@@ -515,7 +589,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
         dprev = d;
     }
 
-    // ---- epilogue: T = 256 C_h + C_l, acc = T 2^(11 - R_n - dmax), the fp32 epilogue ----
+    // ---- epilogue: T = 256 C_h + C_l, acc = T 2^(W - R_n - dmax), the fp32 epilogue ----
     // Each wave's two planes of sums go to LDS column-major (the four rows an MFMA lane holds
     // are contiguous: one 16-byte write each), then a rolled loop over the wave's 16 row groups
     // (lane: row 4 s + lane / 16, columns 4 (lane & 15) .. + 3) forms each output and stores 4
@@ -542,7 +616,7 @@ __global__ __launch_bounds__(512) void gemm4_kernel(Args a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         sw[c] = ftz(sw[c]);
-        sh[c] = W4 - sR[min(nc + c, a.N - 1) - n0] - dmax;
+        sh[c] = WN - sR[min(nc + c, a.N - 1) - n0] - dmax;
     }
     const bool full = m0 + TM <= a.M && n0 + TN <= a.N && a.vec4;
     const bool asc = (a.flags & OTPU_ASCALE) != 0, accf = (a.flags & OTPU_ACC) != 0;
@@ -594,7 +668,8 @@ using namespace otpu;
 int otpu_gemm4_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* da, int64_t ldda, int M, int K,
                    const uint8_t* w, int64_t rs, const uint8_t* ws, int64_t srs, int N, int fmt, int flags, int k0,
                    const float* alpha, float* out, int64_t ors, hipStream_t s) {
-    if ((fmt != OTPU_INT4 && fmt != OTPU_FP4) || M < 16 || (flags & OTPU_RMAX)) return 1;
+    if ((fmt != OTPU_INT4 && fmt != OTPU_FP4 && fmt != OTPU_NVFP4) || M < 16 || (flags & OTPU_RMAX)) return 1;
+    if (fmt == OTPU_NVFP4 && (flags & OTPU_RSC)) return 1;     // (no RSC form: the MM checks refuse it)
     if (((uintptr_t)da & 3) || (ldda % 4) || ((uintptr_t)q & 15) || (ldq % 16) || ((uintptr_t)w & 15) || (rs % 16))
         return 1;
     if (!(flags & OTPU_UNIT) && (((uintptr_t)ws & 3) || (srs % 4))) return 1;
@@ -610,9 +685,12 @@ int otpu_gemm4_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t*
     if (fmt == OTPU_INT4) {
         if (hi) g4::gemm4_kernel<OTPU_INT4, true><<<grid, 512, 0, s>>>(a);
         else g4::gemm4_kernel<OTPU_INT4, false><<<grid, 512, 0, s>>>(a);
-    } else {
+    } else if (fmt == OTPU_FP4) {
         if (hi) g4::gemm4_kernel<OTPU_FP4, true><<<grid, 512, 0, s>>>(a);
         else g4::gemm4_kernel<OTPU_FP4, false><<<grid, 512, 0, s>>>(a);
+    } else {
+        if (hi) g4::gemm4_kernel<OTPU_NVFP4, true><<<grid, 512, 0, s>>>(a);
+        else g4::gemm4_kernel<OTPU_NVFP4, false><<<grid, 512, 0, s>>>(a);
     }
     return otpu_launch_check("mm gemm4");
 }

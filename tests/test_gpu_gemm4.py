@@ -1,8 +1,9 @@
-"""The 4-bit prefill GEMM (int4x / fp4x6 weights, and their RSC / UNIT forms, on the int8 MFMA
-units: csrc/gemm4.hip) against the C oracle bit for bit: single activation planes (ROW), several
-(MX, Horner over the planes), offsets past the window, weight blocks whose offsets spread (the
-folded multipliers), tiles the bounds refuse (the exact VALU path), ACC / ASCALE, k0 column
-slices, ragged tiles, and the c3 shape at full size (`opentpu/isasim.py:749-910`)."""
+"""The 4-bit prefill GEMM (int4x / fp4x6 / nvfp4 weights, and their RSC / UNIT forms, on the int8
+MFMA units: csrc/gemm4.hip) against the C oracle bit for bit: single activation planes (ROW),
+several (MX, Horner over the planes), offsets past the window, weight blocks whose offsets spread
+(the folded multipliers), nvfp4's per-16-group E4M3 scales (subnormal ones included), tiles the
+bounds refuse (the exact VALU path), ACC / ASCALE, k0 column slices, ragged tiles, and the c3
+shape at full size (`opentpu/isasim.py:749-910`)."""
 import sys
 
 import numpy as np
@@ -51,8 +52,11 @@ def activations(rng, M, K, ak):
 
 def weights(rng, N, K, fmt, wk, k0):
     KBr = K // 128 + k0
-    s = {"x4": 1.5, "spread": 2.2, "wide": 4.0}.get(wk, 1.5)
+    s = {"x4": 1.5, "spread": 2.2, "wide": 4.0, "wider": 6.0}.get(wk, 1.5)
     W = (spread(rng, N, KBr * 128, s, 128) * 0.02).astype(np.float32)
+    if wk == "tiny":                                   # 16-groups near zero: subnormal E4M3 scales
+        g = W.reshape(N, -1, 16)
+        g[rng.random(g.shape[:2]) < 0.25] *= np.float32(1e-6)
     rows, srows = Q.quantize_mxu(W, fmt)
     if wk == "rsc":
         srows = np.ascontiguousarray(srows[:, :4])
@@ -82,6 +86,21 @@ CASES = [  # M, N, K, fmt, weights (x4 | spread | wide | rsc | unit), activation
     (200, 256, 1024, "fp4", "x4", (0, 20), 0),      # offsets past the window: those groups drop
     (200, 256, 1024, "int4", "x4", (2, 5, 9), 0),   # drops where d + dw > 11
     (64, 96, 512, "int4", "x4", (20, 30), 0),       # every group drops: zero tiles
+    # nvfp4: 16-groups with an E4M3 scale each, window 13 (no RSC form)
+    (512, 384, 2048, "nvfp4", "x4", "row", 0),
+    (200, 300, 1024, "nvfp4", "x4", "mx", 0),
+    (64, 128, 384, "nvfp4", "x4", "row", 2),
+    (96, 160, 256, "nvfp4", "unit", "mx", 0),
+    (16, 16, 128, "nvfp4", "x4", "row", 0),         # one K stage
+    (33, 40, 256, "nvfp4", "x4", "mx", 0),          # two K stages
+    (50, 64, 384, "nvfp4", "spread", "row", 0),     # three K stages
+    (130, 257, 640, "nvfp4", "tiny", "mx", 0),      # subnormal scales: those groups always drop
+    (80, 96, 1024, "nvfp4", "wide", "row", 0),
+    (80, 96, 1024, "nvfp4", "wider", "row", 0),     # scales past the folding range: VALU
+    (128, 128, 2048, "nvfp4", "x4", "wide", 0),     # activation offsets past the Horner bound: VALU
+    (200, 256, 1024, "nvfp4", "x4", (0, 20), 0),    # offsets past the window: those groups drop
+    (200, 256, 1024, "nvfp4", "x4", (2, 5, 9, 13), 0),   # drops where d + dw > 13
+    (16, 8192, 256, "nvfp4", "x4", "row", 0),       # 64 column tiles: the XCD-major order
 ]
 
 
@@ -98,7 +117,7 @@ def test_gemm4(ops, M, N, K, fmt, wk, ak, k0):
     assert same_bits(got, want)
 
 
-@pytest.mark.parametrize("fmt", ["int4", "fp4"])
+@pytest.mark.parametrize("fmt", ["int4", "fp4", "nvfp4"])
 def test_gemm4_acc_ascale(ops, fmt):
     _, mxu = ops
     rng = np.random.default_rng(9 + len(fmt))
@@ -116,7 +135,7 @@ def test_gemm4_acc_ascale(ops, fmt):
                                 alpha=alpha))
 
 
-@pytest.mark.parametrize("fmt", ["int4", "fp4"])
+@pytest.mark.parametrize("fmt", ["int4", "fp4", "nvfp4"])
 def test_gemm4_c3_full_size(ops, fmt):
     """c3's shape with 4-bit weights: M=512 x K=2048 x N=8192, packed on the GPU from N(0, 0.02),
     ROW and MX activations, every output bit against the C oracle."""
