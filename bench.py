@@ -15,6 +15,7 @@ kernels run on; and the CPU baseline (the C oracle, OpenMP, on this host) on a b
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import os
 import sys
@@ -174,9 +175,9 @@ def lm_head(steps, warmup):
 def gemm(steps, warmup, row_mode=True, fmt="int8", generic=False):
     """The c3 prefill GEMM, RSC weights (fmt int8) or 4-bit group-quantized ones (int4x / fp4x6 / nvfp4:
     the 4-bit GEMM); activations ROW-quantized (the headline: one scale a row, a single exact
-    plane) or MX (group offsets: several planes).  generic: the output rows padded by 4 floats,
-    so that the int8 GEMM runs its generic copy instead of the one compiled for c3's sizes and
-    strides (the same work)."""
+    plane) or MX (group offsets: several planes).  generic: the int8 GEMM's generic copy on the
+    same operands instead of the one compiled for c3's sizes and strides (OTPU_GENERIC_COPIES
+    set while the step is captured; the same work and results)."""
     import torch
 
     from opentpu_amd import _lib as X
@@ -188,16 +189,33 @@ def gemm(steps, warmup, row_mode=True, fmt="int8", generic=False):
     fl = X.RSC if fmt == "int8" else 0
     x = torch.randn((M, K), generator=gen, device="cuda")
     q, Sa, da = fp32.quantize_mx(x, 32, row_mode=row_mode)
-    ors = N + 4 if generic else N
-    obuf = torch.empty((M, ors), dtype=torch.float32, device="cuda")
-    out = obuf[:, :N]
+    out = torch.empty((M, N), dtype=torch.float32, device="cuda")
 
     def step():
         X.call("otpu_mm", X.ptr(q), K, X.ptr(Sa), X.ptr(da), K // 32, M, K, X.ptr(rows), rows.shape[1], X.ptr(srows),
-               srows.shape[1], N, X.FMT[fmt], fl, 0, None, X.ptr(out), ors, None, X.stream())
-    ms = timed(step, steps, warmup, torch.cuda.current_stream())
-    sample = tuple(t.cpu().numpy() for t in (q, Sa, da, rows, srows, out.contiguous()))
+               srows.shape[1], N, X.FMT[fmt], fl, 0, None, X.ptr(out), N, None, X.stream())
+    with generic_copies(generic):
+        ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    sample = tuple(t.cpu().numpy() for t in (q, Sa, da, rows, srows, out))
     return ms, sample
+
+
+@contextlib.contextmanager
+def generic_copies(on):
+    """OTPU_GENERIC_COPIES set inside (when on): the library then launches its generic kernel
+    copies instead of the ones compiled for the c3 / c4 shapes (read per GEMM call and when a
+    chain's plan is built; the same work and results)."""
+    old = os.environ.get("OTPU_GENERIC_COPIES")
+    if on:
+        os.environ["OTPU_GENERIC_COPIES"] = "1"
+    try:
+        yield
+    finally:
+        if on:
+            if old is None:
+                del os.environ["OTPU_GENERIC_COPIES"]
+            else:
+                os.environ["OTPU_GENERIC_COPIES"] = old
 
 
 def int_mm(steps, warmup):
@@ -212,11 +230,12 @@ def int_mm(steps, warmup):
     return timed(lambda: torch._int_mm(A, Bw.t(), out=C), steps, warmup, torch.cuda.current_stream())
 
 
-def c4_step(steps, warmup, persistent=True):
+def c4_step(steps, warmup, persistent=True, generic=False):
     """The chained decode step (28 Qwen3-0.6B-shaped layers of int4x linears, weights seeded
     100 + layer): two resident copies of the weights (474 MB, more than the Infinity Cache),
     steps alternating between them, every step's kernels replayed from one HIP graph.
-    persistent: the step as one otpu_chain_step launch (the default path), else 112 launches."""
+    persistent: the step as one otpu_chain_step launch (the default path), else 112 launches.
+    generic: the persistent kernel's generic copy instead of the one compiled for this shape."""
     import torch
 
     from opentpu_amd.chain import DecodeChain, Shape
@@ -232,7 +251,8 @@ def c4_step(steps, warmup, persistent=True):
     def step():
         chains[it[0] % 2].step()
         it[0] += 1
-    ms = timed(step, steps, warmup, torch.cuda.current_stream())
+    with generic_copies(generic):                   # (the plans are built at the first step)
+        ms = timed(step, steps, warmup, torch.cuda.current_stream())
     for c in chains:                    # a step whose hand-off waits gave up is no measurement
         c.check()
     wb = sh.layers * sh.layer_bytes("int4")
@@ -514,6 +534,9 @@ def main():
         # the same step as one launch per linear (the path the persistent step replaces)
         extra["c4_decode_step_launches"] = c4_step(10, 2, persistent=False)
         print(f"[c4 launches] {extra['c4_decode_step_launches']}", file=sys.stderr, flush=True)
+        # the persistent step's generic copy (what every other shape runs) on the same weights
+        extra["c4_decode_step_generic_copy"] = c4_step(10, 2, generic=True)
+        print(f"[c4 generic copy] {extra['c4_decode_step_generic_copy']}", file=sys.stderr, flush=True)
         if not args.no_cpu:
             samples["c4"] = c4_layer_sample()
     if "c3" in only or "c3r" in only:

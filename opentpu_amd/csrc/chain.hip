@@ -82,6 +82,7 @@ struct ChainPlan {                               // device memory: the header, t
     int norms;                                   // 0 no RSCALE / CSCALE factors, 1 some, 2 both in every layer
     int spin;                                    // polls a wait allows
     int combo;                                   // the phases' pieces a lane: 0 (LQ, LO, LF) = (1, 1, 2), 1 (2, 1, 4)
+    int generic;                                 // never the C4 copy (OTPU_GENERIC_COPIES at plan time)
     uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
 };
 
@@ -117,6 +118,29 @@ __device__ __forceinline__ T cload(const T& r) {
 #endif
 }
 
+// a phase's argument block, field by field through cload: a copy of the whole struct through
+// the constant address space is lowered to vector loads, whose waits (vmcnt counts stores as
+// well) also held each phase until the previous phase's output stores were acknowledged,
+// before any of its weight loads issued.  Only the fields a phase uses are loaded.
+__device__ __forceinline__ MMArgs cload_args(const MMArgs& r) {
+    static_assert(sizeof(MMArgs) == 336, "every field of MMArgs copied below");
+    MMArgs a;
+    a.q = cload(r.q); a.ldq = cload(r.ldq); a.Sa = cload(r.Sa); a.da = cload(r.da); a.ldda = cload(r.ldda);
+    a.M = cload(r.M); a.K = cload(r.K); a.w = cload(r.w); a.rs = cload(r.rs); a.ws = cload(r.ws);
+    a.srs = cload(r.srs); a.N = cload(r.N); a.flags = cload(r.flags); a.k0 = cload(r.k0);
+    a.alpha = cload(r.alpha); a.out = cload(r.out); a.ors = cload(r.ors); a.rmax_key = cload(r.rmax_key);
+    a.acc_out = cload(r.acc_out); a.best = cload(r.best); a.base = cload(r.base); a.P = cload(r.P);
+    a.T = cload(r.T); a.nseg = cload(r.nseg); a.q_bs = cload(r.q_bs); a.sa_bs = cload(r.sa_bs);
+    a.da_bs = cload(r.da_bs); a.w_bs = cload(r.w_bs); a.ws_bs = cload(r.ws_bs); a.out_bs = cload(r.out_bs);
+    a.k0_bs = cload(r.k0_bs); a.xin = cload(r.xin); a.xmul = cload(r.xmul); a.rscale = cload(r.rscale);
+    a.cscale = cload(r.cscale); a.nsum = cload(r.nsum); a.sum_stride = cload(r.sum_stride);
+    a.xin_bs = cload(r.xin_bs); a.ll_in = cload(r.ll_in); a.ll_out = cload(r.ll_out);
+    a.tag_in = cload(r.tag_in); a.tag_out = cload(r.tag_out); a.err = cload(r.err); a.spin = cload(r.spin);
+    a.ll_all = cload(r.ll_all); a.gu_pair = cload(r.gu_pair); a.fold_c = cload(r.fold_c);
+    a.stamp = cload(r.stamp);
+    return a;
+}
+
 // NORMS: 0 no RSCALE / CSCALE factors (constant NULLs), 1 some, 2 both in every layer (the
 // prologues' tests of the factors drop out).  LQ, LO, LF: the 16-byte pieces a lane holds in
 // the q/k/v and gate/up phases (32 lanes a row: hidden <= 1024 LQ), in o (64 lanes: q_dim <=
@@ -134,12 +158,13 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
 #pragma unroll 1
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * l + k;
-            MMArgs a = cload(P.kind[k]);
+            MMArgs a = cload_args(P.kind[k]);
             // stamps: 0 phase start, 1 weights issued (the wait starts), 2 input row in, 3 QACT
             // done, 4 rows stored
             uint64_t* const st = cload(P.stamps);
             a.stamp = st ? st + ((int64_t)i * gridDim.x + b) * 8 : nullptr;
             OTPU_STAMP(a, 0);
+            if (C4) a.N = k == 0 ? 4096 : k == 2 ? 6144 : 1024;
             if (b * rows_per_wg(k) >= a.N) continue;     // no rows here: nothing to wait for
             a.w = cload(ly.w[k]);
             a.ws = cload(ly.ws[k]);
@@ -184,8 +209,12 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
                 const uint8_t* const next = cload(LY[l + 1 < NL ? l + 1 : l].w[0]);
                 fold_body<FMT, LF, DN_T, true>(a, &lds.f);
                 asm volatile("" ::"s"(next));
-            } else if (C4 && k == 0) {                   // (its own call site: its constants)
-                if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 4096; a.gu_pair = 0; a.rs = 512; a.srs = 40; }
+            } else if (C4 && (k == 0 || k == 2)) {      // q/k/v and gate/up: one call site, one body
+                if constexpr (C4) {
+                    a.K = 1024; a.P = 32; a.rs = 512; a.srs = 40;
+                    a.N = k == 0 ? 4096 : 6144;
+                    a.gu_pair = k == 0 ? 0 : 3072;
+                }
                 if (i == 0) gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, false, NRM>(a, &lds.q);   // plain x0
                 else gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
             } else if (k == 2) {
@@ -207,7 +236,7 @@ __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
     __shared__ __align__(16) ChainLds lds;
     const ChainPlan& P = *plan;
     const bool fixed = P.spin == CHAIN_SPIN;
-    const bool c4 = OTPU_CHAIN_C4 && fixed && P.combo == 0 && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 &&
+    const bool c4 = OTPU_CHAIN_C4 && fixed && !P.generic && P.combo == 0 && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 &&
                     P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && P.kind[3].fold_c == 1 && !P.kv_wait &&
                     P.kind[0].rs == 512 && P.kind[0].srs == 40 && P.kind[1].rs == 1024 && P.kind[1].srs == 72 &&
                     P.kind[2].rs == 512 && P.kind[2].srs == 40 && P.kind[3].rs == 1536 && P.kind[3].srs == 104;
@@ -386,6 +415,7 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
     }
     // the waits' poll limit: OTPU_CHAIN_SPIN (0 .. 2^20) overrides it, e.g. to drive the timeout
     // path from the host in a test (every wait then gives up at once and sets the error word)
+    hp.generic = getenv("OTPU_GENERIC_COPIES") != nullptr;
     hp.spin = CHAIN_SPIN;
     if (const char* e = getenv("OTPU_CHAIN_SPIN")) {
         const long v = strtol(e, nullptr, 10);

@@ -19,6 +19,8 @@
 // ds_read_b128 of a 16-row fragment hits distinct banks).  Each wave computes 64 x 64 with
 // 4 x 4 v_mfma_i32_16x16x64_i8.  Tiles are assigned XCD-major: the workgroups of one XCD
 // share weight rows, so each weight panel is fetched from HBM once into that XCD's L2.
+#include <cstdlib>
+
 #include "otpu_common.h"
 
 namespace otpu {
@@ -1174,8 +1176,10 @@ int otpu_gemm_try(const int8_t* q, int64_t ldq, const float* Sa, const uint8_t* 
     a.tiles_m = (M + GBM - 1) / GBM;
     a.tiles_n = (N + GBN - 1) / GBN;
     a.vec4 = ((uintptr_t)out % 16 == 0) && (ors % 4 == 0);
+    // (OTPU_GENERIC_COPIES set: the generic copy for every shape, the same results; for measuring
+    // what the c3 copy is worth on the same operands)
     const bool c3 = OTPU_GEMM_C3 && M == 512 && N == 8192 && K == 2048 && ldq == 2048 && rs == 2048 && ldda == 64 &&
-                    srs == 4 && ors == 8192 && a.vec4;
+                    srs == 4 && ors == 8192 && a.vec4 && !getenv("OTPU_GENERIC_COPIES");
     if (OTPU_GEMM_LW) {
         if (c3) gemm_lw_kernel<true><<<a.tiles_m * a.tiles_n, 512, 0, s>>>(a);
         else gemm_lw_kernel<false><<<a.tiles_m * a.tiles_n, 512, 0, s>>>(a);

@@ -290,7 +290,7 @@ def test_chain_with_norms(X):
     assert ch.chain_error() == 0
 
 
-def test_chain_c4_full_and_graph(X):
+def test_chain_c4_full_and_graph(X, monkeypatch):
     """The c4 workload (28 layers, Qwen3-0.6B linears, int4x weights seeded 100 + layer): the
     eager step and three replays of its HIP graph (with eager work between them) all equal the
     oracle's step bit for bit; the first layers' outputs are not all zero."""
@@ -318,6 +318,13 @@ def test_chain_c4_full_and_graph(X):
     assert ch.fold and ch.persistent and ch.kernels_per_step == 1
     assert same_bits(ch.step(x).cpu().numpy(), want)
     assert ch.chain_error() == 0
+    say("chain c4: eager step, the persistent kernel's generic copy (OTPU_GENERIC_COPIES at plan time)")
+    monkeypatch.setenv("OTPU_GENERIC_COPIES", "1")
+    ch._plan = None                                # (a plan reads the setting when it is built)
+    assert same_bits(ch.step(x).cpu().numpy(), want)
+    assert ch.chain_error() == 0
+    monkeypatch.delenv("OTPU_GENERIC_COPIES")
+    ch._plan = None
     ch.persistent = False
     assert ch.kernels_per_step == 112
     assert same_bits(ch.step(x).cpu().numpy(), want)

@@ -517,10 +517,14 @@ def test_gemm_c3_shape_tile_kinds(ops):
     assert not np.any(got[256:384]), "offsets past the window: the tile drops every group"
 
 
-def test_gemm_c3_full_size(ops):
+@pytest.mark.parametrize("generic", [False, True])
+def test_gemm_c3_full_size(ops, monkeypatch, generic):
     """c3: M=512 x K=2048 x N=8192, ROW activations x RSC weights (the headline GEMM) and MX
-    activations (the plane path), every output bit against the C oracle."""
+    activations (the plane path), every output bit against the C oracle; with the copy compiled
+    for c3's sizes and with the generic copy on the same operands (OTPU_GENERIC_COPIES)."""
     import torch
+    if generic:
+        monkeypatch.setenv("OTPU_GENERIC_COPIES", "1")
     _, quant, mxu = ops
     M, K, N = 512, 2048, 8192
     gen = torch.Generator(device="cuda").manual_seed(3)
@@ -530,7 +534,7 @@ def test_gemm_c3_full_size(ops):
     x = np.random.default_rng(3).standard_normal((M, K)).astype(np.float32)
     for row_mode in (True, False):
         q, Sa, da = F.quantize_mx(x, 32, row_mode=row_mode)
-        say("gemm c3", "row" if row_mode else "mx")
+        say("gemm c3", "row" if row_mode else "mx", "generic copy" if generic else "c3 copy")
         got = mxu.mm(q, Sa, da, rows, srows, "int8", K, rsc=True)
         want = OC.mm(q, Sa, da, rows, srows, "int8", K, flags=MM.RSC)
         assert same_bits(got, want)
