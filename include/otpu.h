@@ -203,10 +203,12 @@ int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float
  *   one and two pieces a lane, larger shapes up to Qwen3-1.7B's two and four), hidden and q_dim
  *   multiples of 32.
  *   otpu_chain_step: one step (reads x, writes every output row); capturable in a HIP graph.
- *   Steps on one plan must not overlap (issue them on one stream).  A step needs all of its
- *   workgroups (one a CU) resident at once: the plan and the step refuse (OTPU_ELAUNCH) a
- *   device whose occupancy for the kernel cannot hold them; kernels beside it on other streams
- *   can still hold CUs back, and its waits then run out of polls (they are bounded: no hang).
+ *   Steps on one plan must not overlap (issue them on one stream).  It launches the kernel
+ *   otpu_chain_plan picked for the plan (a plan built at that address in this process; else
+ *   OTPU_EINVAL).  A step needs all of its workgroups (one a CU) resident at once: the plan
+ *   refuses (OTPU_ELAUNCH) a device whose occupancy for its kernel cannot hold them; kernels
+ *   beside it on other streams can still hold CUs back, and its waits then run out of polls
+ *   (they are bounded: no hang).
  *   otpu_chain_error: the plan's error word (0: every hand-off completed; 1: a wait ran out of
  *   polls, the outputs since are invalid), synchronous.  It stays set until the plan is
  *   written again. */

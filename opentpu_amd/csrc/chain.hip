@@ -28,6 +28,8 @@
 #include <algorithm>
 #include <cstddef>
 #include <cstdlib>
+#include <mutex>
+#include <unordered_map>
 #include <vector>
 
 #include "gemv_fold.h"
@@ -232,37 +234,48 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     if (threadIdx.x == 0) __hip_atomic_store(P.calls + b, E + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// One kernel per compiled copy of the step, each its own function: as copies of one kernel, the
+// code of each moved whenever another was added (the C4 copy measured 358 -> 363 us a step with
+// an unused copy compiled in beside it).  otpu_chain_plan picks the kernel (chain_pick) and
+// otpu_chain_step launches it.
+template <int FMT, bool FIXED, bool C4, int NORMS, int LQ, int LO, int LF>
 __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
     __shared__ __align__(16) ChainLds lds;
-    const ChainPlan& P = *plan;
+    chain_run<FMT, FIXED, C4, NORMS, LQ, LO, LF>(*plan, lds);
+}
+
+// the C4 copy's shape: Qwen3-0.6B's phases (hidden 1024, q_dim 2048, kv_dim 1024, F 3072, dense
+// 4-bit rows and scale rows)
+static bool is_c4_shape(const ChainPlan& P) {
+    return P.combo == 0 && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 && P.kind[1].N == 1024 &&
+           P.kind[2].N == 6144 && P.kind[3].K == 3072 && P.kind[3].fold_c == 1 && !P.kv_wait &&
+           P.kind[0].rs == 512 && P.kind[0].srs == 40 && P.kind[1].rs == 1024 && P.kind[1].srs == 72 &&
+           P.kind[2].rs == 512 && P.kind[2].srs == 40 && P.kind[3].rs == 1536 && P.kind[3].srs == 104;
+}
+
+// the kernel for a plan: the format; the poll limit a constant (FIXED) or the plan's; the C4
+// copy where the shape is Qwen3-0.6B's (and OTPU_GENERIC_COPIES was not set); the norm factors
+// none / some / both in every layer; the phases' pieces a lane (combo)
+template <int FMT>
+static const void* chain_pick_fmt(const ChainPlan& P) {
     const bool fixed = P.spin == CHAIN_SPIN;
-    const bool c4 = OTPU_CHAIN_C4 && fixed && !P.generic && P.combo == 0 && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 &&
-                    P.kind[1].N == 1024 && P.kind[2].N == 6144 && P.kind[3].K == 3072 && P.kind[3].fold_c == 1 && !P.kv_wait &&
-                    P.kind[0].rs == 512 && P.kind[0].srs == 40 && P.kind[1].rs == 1024 && P.kind[1].srs == 72 &&
-                    P.kind[2].rs == 512 && P.kind[2].srs == 40 && P.kind[3].rs == 1536 && P.kind[3].srs == 104;
-    if (P.combo == 1) {                          // hidden <= 2048, q_dim <= 2048, F <= 8192
-        if (P.fmt == OTPU_INT4) {
-            if (fixed) chain_run<OTPU_INT4, true, false, 1, 2, 1, 4>(P, lds);
-            else chain_run<OTPU_INT4, false, false, 1, 2, 1, 4>(P, lds);
-        } else {
-            if (fixed) chain_run<OTPU_FP4, true, false, 1, 2, 1, 4>(P, lds);
-            else chain_run<OTPU_FP4, false, false, 1, 2, 1, 4>(P, lds);
-        }
-        return;
-    }
-    if (P.fmt == OTPU_INT4) {
-        if (c4 && P.norms == 0) chain_run<OTPU_INT4, true, true, 0>(P, lds);
-        else if (c4 && P.norms == 2) chain_run<OTPU_INT4, true, true, 2>(P, lds);
-        else if (c4) chain_run<OTPU_INT4, true, true, 1>(P, lds);
-        else if (fixed) chain_run<OTPU_INT4, true, false, 1>(P, lds);
-        else chain_run<OTPU_INT4, false, false, 1>(P, lds);
-    } else {
-        if (c4 && P.norms == 0) chain_run<OTPU_FP4, true, true, 0>(P, lds);
-        else if (c4 && P.norms == 2) chain_run<OTPU_FP4, true, true, 2>(P, lds);
-        else if (c4) chain_run<OTPU_FP4, true, true, 1>(P, lds);
-        else if (fixed) chain_run<OTPU_FP4, true, false, 1>(P, lds);
-        else chain_run<OTPU_FP4, false, false, 1>(P, lds);
-    }
+    if (!fixed)
+        return P.combo == 1 ? (const void*)chain_kernel<FMT, false, false, 1, 2, 1, 4>
+                            : (const void*)chain_kernel<FMT, false, false, 1, 1, 1, DN_L>;
+    if (P.combo == 1)
+        return P.norms == 0 ? (const void*)chain_kernel<FMT, true, false, 0, 2, 1, 4>
+             : P.norms == 2 ? (const void*)chain_kernel<FMT, true, false, 2, 2, 1, 4>
+                            : (const void*)chain_kernel<FMT, true, false, 1, 2, 1, 4>;
+    if (OTPU_CHAIN_C4 && !P.generic && is_c4_shape(P))
+        return P.norms == 0 ? (const void*)chain_kernel<FMT, true, true, 0, 1, 1, DN_L>
+             : P.norms == 2 ? (const void*)chain_kernel<FMT, true, true, 2, 1, 1, DN_L>
+                            : (const void*)chain_kernel<FMT, true, true, 1, 1, 1, DN_L>;
+    return P.norms == 0 ? (const void*)chain_kernel<FMT, true, false, 0, 1, 1, DN_L>
+         : P.norms == 2 ? (const void*)chain_kernel<FMT, true, false, 2, 1, 1, DN_L>
+                        : (const void*)chain_kernel<FMT, true, false, 1, 1, 1, DN_L>;
+}
+static const void* chain_pick(const ChainPlan& P) {
+    return P.fmt == OTPU_INT4 ? chain_pick_fmt<OTPU_INT4>(P) : chain_pick_fmt<OTPU_FP4>(P);
 }
 
 static int64_t rnd256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -284,40 +297,35 @@ static ChainLayout chain_layout(int layers, int maxn) {
 
 using namespace otpu;
 
+// The kernel each plan was built for, by the plan's device address (set by otpu_chain_plan; a
+// plan rebuilt at the same address replaces its entry), with the dynamic LDS it launches with.
+struct ChainPick {
+    const void* fn;
+    int pad;
+};
+static std::mutex chain_mu;
+static std::unordered_map<uintptr_t, ChainPick> chain_picks;
+
 // The step's dynamic LDS: one workgroup a CU (the padding leaves room for no second; without it
 // the workgroups are resident all the same, some sharing a CU).
-static int chain_pad() {
-    static const int pad = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(chain_kernel),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, CHAIN_PAD_LDS) == hipSuccess
-                   ? CHAIN_PAD_LDS : 0;
-    }();
-    return pad;
+static int chain_pad(const void* fn) {
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, CHAIN_PAD_LDS) == hipSuccess
+               ? CHAIN_PAD_LDS : 0;
 }
 
 // The step's workgroups wait on each other's rows, so all of them must be resident at once: the
 // occupancy the compiled kernel allows with its LDS, times the CUs, must cover the grid of one
-// workgroup a CU.  Checked once per device (the kernel's resources do not change); a device where
-// it does not hold refuses plans and steps instead of running into the waits' time-out.
-static int chain_resident_check(const char* what) {
-    static int cache[64] = {0};                          // 0 unknown, else 1 + workgroups a CU
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
-        return otpu_fail(OTPU_ENODEV, "%s: no current device", what);
-    int v = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
-    if (v == 0) {
-        int per_cu = 0;
-        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(chain_kernel), 256, chain_pad());
-        if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "%s: occupancy query: %s", what, hipGetErrorString(e));
-        v = 1 + (per_cu > 0 ? per_cu : 0);
-        __atomic_store_n(&cache[dev], v, __ATOMIC_RELAXED);
-    }
+// workgroup a CU.  Checked when a plan is built (a plan serves the device current then); a device
+// where it does not hold refuses the plan instead of running into the waits' time-out.
+static int chain_resident_check(const char* what, const void* fn, int pad) {
+    int per_cu = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, pad);
+    if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "%s: occupancy query: %s", what, hipGetErrorString(e));
     // (one workgroup a CU: the grid is the CU count)
-    if (v - 1 < 1)
+    if (per_cu < 1)
         return otpu_fail(OTPU_ELAUNCH,
                          "%s: the persistent step's %d workgroups cannot all be resident at once on this "
-                         "device (%d a CU); use the launch-per-linear path", what, otpu_cu_count(), v - 1);
+                         "device (%d a CU); use the launch-per-linear path", what, otpu_cu_count(), per_cu);
     return OTPU_OK;
 }
 
@@ -348,7 +356,6 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
         return otpu_fail(OTPU_EINVAL, "chain_plan: %lld bytes, the plan needs %lld", (long long)plan_bytes,
                          (long long)lay.total);
     if (otpu_cu_count() > CHAIN_SLOTS) return otpu_fail(OTPU_EINVAL, "chain_plan: more than %d CUs", CHAIN_SLOTS);
-    if (int rc = chain_resident_check("chain_plan")) return rc;
     // each phase kind checked and built as its one-launch entry point would (layer 0's
     // pointers); then every layer's pointers checked the same way
     const int Ns[4] = {nq, hidden, 2 * F, hidden}, Ks[4] = {hidden, q_dim, hidden, F};
@@ -421,19 +428,36 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
         const long v = strtol(e, nullptr, 10);
         if (v >= 0 && v <= (1 << 20)) hp.spin = (int)v;
     }
+    // the kernel compiled for this plan, and whether its workgroups fit the device at once
+    const ChainPick pick = {chain_pick(hp), 0};
+    const ChainPick pk = {pick.fn, chain_pad(pick.fn)};
+    if (int rc = chain_resident_check("chain_plan", pk.fn, pk.pad)) return rc;
     // synchronous copies: a plan is built once, outside any capture
     hipError_t e = hipMemset(base, 0, (size_t)lay.total);
     if (e == hipSuccess) e = hipMemcpy(base, &hp, sizeof(hp), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(base + lay.layer, ly.data(), sizeof(ChainLayer) * layers, hipMemcpyHostToDevice);
     if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "chain_plan: %s", hipGetErrorString(e));
+    {
+        std::lock_guard<std::mutex> g(chain_mu);
+        chain_picks[(uintptr_t)plan] = pk;
+    }
     return OTPU_OK;
 }
 
 extern "C" int otpu_chain_step(const void* plan, otpu_stream_t stream) {
     if (!plan || (uintptr_t)plan % 256) return otpu_fail(OTPU_EINVAL, "chain_step: plan NULL or misaligned");
-    if (int rc = chain_resident_check("chain_step")) return rc;
-    chain_kernel<<<(unsigned)otpu_cu_count(), 256, chain_pad(), (hipStream_t)stream>>>(
-        static_cast<const ChainPlan*>(plan));
+    ChainPick pk = {nullptr, 0};
+    {
+        std::lock_guard<std::mutex> g(chain_mu);
+        const auto it = chain_picks.find((uintptr_t)plan);
+        if (it != chain_picks.end()) pk = it->second;
+    }
+    if (!pk.fn) return otpu_fail(OTPU_EINVAL, "chain_step: no plan built at %p by otpu_chain_plan in this process", plan);
+    const ChainPlan* P = static_cast<const ChainPlan*>(plan);
+    void* args[] = {&P};
+    const hipError_t e = hipLaunchKernel(pk.fn, dim3((unsigned)otpu_cu_count()), dim3(256), args, (size_t)pk.pad,
+                                         (hipStream_t)stream);
+    if (e != hipSuccess) return otpu_fail(OTPU_ELAUNCH, "chain_step: %s", hipGetErrorString(e));
     return otpu_launch_check("chain_step");
 }
 
