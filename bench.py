@@ -230,16 +230,17 @@ def int_mm(steps, warmup):
     return timed(lambda: torch._int_mm(A, Bw.t(), out=C), steps, warmup, torch.cuda.current_stream())
 
 
-def c4_step(steps, warmup, persistent=True, generic=False):
+def c4_step(steps, warmup, persistent=True, generic=False, shape=None):
     """The chained decode step (28 Qwen3-0.6B-shaped layers of int4x linears, weights seeded
     100 + layer): two resident copies of the weights (474 MB, more than the Infinity Cache),
     steps alternating between them, every step's kernels replayed from one HIP graph.
     persistent: the step as one otpu_chain_step launch (the default path), else 112 launches.
-    generic: the persistent kernel's generic copy instead of the one compiled for this shape."""
+    generic: the persistent kernel's generic copy instead of the one compiled for this shape.
+    shape: another layer shape (chain.Shape) than Qwen3-0.6B's, 28 layers."""
     import torch
 
     from opentpu_amd.chain import DecodeChain, Shape
-    sh = Shape()
+    sh = shape or Shape()
     chains = [DecodeChain.synthetic(sh, "int4", seed0=100) for _ in range(2)]
     for c in chains:
         c.persistent = persistent
@@ -537,6 +538,11 @@ def main():
         # the persistent step's generic copy (what every other shape runs) on the same weights
         extra["c4_decode_step_generic_copy"] = c4_step(10, 2, generic=True)
         print(f"[c4 generic copy] {extra['c4_decode_step_generic_copy']}", file=sys.stderr, flush=True)
+        # the persistent step at Qwen3-1.7B's layer shape (hidden 2048, q_dim 2048, kv_dim 1024,
+        # F 6144: 768-column down chunks), 28 layers: the chain's second set of teams
+        from opentpu_amd.chain import Shape
+        extra["c4_qwen3_1p7b_shape_step"] = c4_step(10, 2, shape=Shape(hidden=2048, q_dim=2048, kv_dim=1024, F=6144))
+        print(f"[c4 1.7B shape] {extra['c4_qwen3_1p7b_shape_step']}", file=sys.stderr, flush=True)
         if not args.no_cpu:
             samples["c4"] = c4_layer_sample()
     if "c3" in only or "c3r" in only:

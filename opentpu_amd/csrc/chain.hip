@@ -100,11 +100,26 @@ union ChainLds {
 
 // FIXED: the default poll limit as a constant (folded into the waits: a limit read from the plan
 // measured 16 us a step slower); the other copy serves plans with an OTPU_CHAIN_SPIN override.
-// C4: a copy for the Qwen3-0.6B shape (hidden 1024, q_dim 2048, kv_dim 1024, F 3072), its
-// phases' K, pieces and rows as constants
+// SH: a copy for one layer shape, its phases' K, pieces, rows and strides as constants (0: the
+// generic copy, which reads them from the plan; OTPU_CHAIN_C4=0 builds no shape copies)
 #ifndef OTPU_CHAIN_C4
 #define OTPU_CHAIN_C4 1
 #endif
+struct ChainShape {
+    int K[4], P[4], N[4], rs[4], srs[4];         // per phase: qkv, o, gu, down
+    int gu_pair, fold_c;                         // gate/up's pairs (F); the fold's sub-ranges a range
+    int combo;                                   // the teams it runs (ChainPlan::combo)
+};
+// 4-bit rows of K / 2 bytes (K / 32 pieces), scale rows of 8 + 8 ceil(K / 256) bytes
+constexpr ChainShape CHAIN_SHAPES[3] = {
+    {},                                          // 0: the generic copy
+    // 1: Qwen3-0.6B (hidden 1024, q_dim 2048, kv_dim 1024, F 3072: down chunks of 256)
+    {{1024, 2048, 1024, 3072}, {32, 64, 32, 96}, {4096, 1024, 6144, 1024}, {512, 1024, 512, 1536},
+     {40, 72, 40, 104}, 3072, 1, 0},
+    // 2: Qwen3-1.7B (hidden 2048, q_dim 2048, kv_dim 1024, F 6144: down chunks of 768)
+    {{2048, 2048, 2048, 6144}, {64, 64, 64, 192}, {4096, 2048, 12288, 2048}, {1024, 1024, 1024, 3072},
+     {72, 72, 72, 200}, 6144, 3, 1},
+};
 
 // a field of the plan or of its layer table, read through the constant address space: the
 // plan does not change while a step runs (only what its pointers point to), and the compiler,
@@ -147,9 +162,10 @@ __device__ __forceinline__ MMArgs cload_args(const MMArgs& r) {
 // prologues' tests of the factors drop out).  LQ, LO, LF: the 16-byte pieces a lane holds in
 // the q/k/v and gate/up phases (32 lanes a row: hidden <= 1024 LQ), in o (64 lanes: q_dim <=
 // 2048 LO) and in the fold (64 lanes: F <= 2048 LF)
-template <int FMT, bool FIXED, bool C4, int NORMS, int LQ = 1, int LO = 1, int LF = DN_L>
+template <int FMT, bool FIXED, int SH, int NORMS, int LQ = 1, int LO = 1, int LF = DN_L>
 __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
     constexpr int NRM = NORMS == 0 ? 1 : NORMS == 2 ? 2 : 0;    // the prologues' factor flag
+    constexpr ChainShape S = CHAIN_SHAPES[SH];
     const int b = blockIdx.x;
     const uint32_t E = __hip_atomic_load(P.calls + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int NL = cload(P.layers);
@@ -166,7 +182,10 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             uint64_t* const st = cload(P.stamps);
             a.stamp = st ? st + ((int64_t)i * gridDim.x + b) * 8 : nullptr;
             OTPU_STAMP(a, 0);
-            if (C4) a.N = k == 0 ? 4096 : k == 2 ? 6144 : 1024;
+            // (a select on k, not S.N[k]: indexed by the loop's k, the table read became a switch, and
+            // the compiler then copied the rest of the phase's code for each k)
+            static_assert(S.N[1] == S.N[3], "o and the down projection both write the hidden row");
+            if (SH) a.N = k == 0 ? S.N[0] : k == 2 ? S.N[2] : S.N[1];
             if (b * rows_per_wg(k) >= a.N) continue;     // no rows here: nothing to wait for
             a.w = cload(ly.w[k]);
             a.ws = cload(ly.ws[k]);
@@ -198,29 +217,29 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
                 a.rscale = rn ? rn + 2 * l + (k >> 1) : nullptr;
                 a.cscale = cload(ly.cs[k >> 1]);
             }
-            // (C4: 4-bit rows of K / 2 bytes, scale rows of 8 + 8 ceil(K / 256) bytes)
             if (k == 1) {
                 if (cload(P.kv_wait)) a.ll_all = cload(P.kind[0].N);   // o waits for k and v too
-                if constexpr (C4) { a.K = 2048; a.P = 64; a.N = 1024; a.ll_all = 0; a.rs = 1024; a.srs = 72; }
+                if constexpr (SH != 0) { a.K = S.K[1]; a.P = S.P[1]; a.N = S.N[1]; a.ll_all = 0; a.rs = S.rs[1]; a.srs = S.srs[1]; }
                 gemv_body<FMT, 1, LO, O_T, false, true, O_R, true, true, 1>(a, &lds.q);
             } else if (k == 3) {
-                if constexpr (C4) { a.K = 3072; a.P = 96; a.N = 1024; a.rs = 1536; a.srs = 104; a.fold_c = 1; }
+                if constexpr (SH != 0) { a.K = S.K[3]; a.P = S.P[3]; a.N = S.N[3]; a.rs = S.rs[3]; a.srs = S.srs[3]; a.fold_c = S.fold_c; }
                 // the next layer's table line read into the scalar cache during the fold, so that
                 // its first phase finds its weight pointers there (the empty asm keeps the load;
                 // its wait falls after the fold's own waits): ~1.5 us a step
                 const uint8_t* const next = cload(LY[l + 1 < NL ? l + 1 : l].w[0]);
                 fold_body<FMT, LF, DN_T, true>(a, &lds.f);
                 asm volatile("" ::"s"(next));
-            } else if (C4 && (k == 0 || k == 2)) {      // q/k/v and gate/up: one call site, one body
-                if constexpr (C4) {
-                    a.K = 1024; a.P = 32; a.rs = 512; a.srs = 40;
-                    a.N = k == 0 ? 4096 : 6144;
-                    a.gu_pair = k == 0 ? 0 : 3072;
+            } else if (SH != 0 && (k == 0 || k == 2)) { // q/k/v and gate/up: one call site, one body
+                if constexpr (SH != 0) {
+                    static_assert(S.K[0] == S.K[2] && S.P[0] == S.P[2] && S.rs[0] == S.rs[2] && S.srs[0] == S.srs[2],
+                                  "q/k/v and gate/up share their K");
+                    a.K = S.K[0]; a.P = S.P[0]; a.rs = S.rs[0]; a.srs = S.srs[0];
+                    a.N = k == 0 ? S.N[0] : S.N[2];
+                    a.gu_pair = k == 0 ? 0 : S.gu_pair;
                 }
                 if (i == 0) gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, false, NRM>(a, &lds.q);   // plain x0
                 else gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
             } else if (k == 2) {
-                if constexpr (C4) { a.K = 1024; a.P = 32; a.N = 6144; a.gu_pair = 3072; a.rs = 512; a.srs = 40; }
                 gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
             } else if (i == 0) {                         // the step's first phase reads the plain x0
                 gemv_body<FMT, 1, LQ, QKV_T, false, true, QKV_R, true, false, NRM>(a, &lds.q);
@@ -238,41 +257,42 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
 // code of each moved whenever another was added (the C4 copy measured 358 -> 363 us a step with
 // an unused copy compiled in beside it).  otpu_chain_plan picks the kernel (chain_pick) and
 // otpu_chain_step launches it.
-template <int FMT, bool FIXED, bool C4, int NORMS, int LQ, int LO, int LF>
+template <int FMT, bool FIXED, int SH, int NORMS, int LQ, int LO, int LF>
 __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
     __shared__ __align__(16) ChainLds lds;
-    chain_run<FMT, FIXED, C4, NORMS, LQ, LO, LF>(*plan, lds);
+    chain_run<FMT, FIXED, SH, NORMS, LQ, LO, LF>(*plan, lds);
 }
 
-// the C4 copy's shape: Qwen3-0.6B's phases (hidden 1024, q_dim 2048, kv_dim 1024, F 3072, dense
-// 4-bit rows and scale rows)
-static bool is_c4_shape(const ChainPlan& P) {
-    return P.combo == 0 && P.kind[0].K == 1024 && P.kind[0].N == 4096 && P.kind[1].K == 2048 && P.kind[1].N == 1024 &&
-           P.kind[2].N == 6144 && P.kind[3].K == 3072 && P.kind[3].fold_c == 1 && !P.kv_wait &&
-           P.kind[0].rs == 512 && P.kind[0].srs == 40 && P.kind[1].rs == 1024 && P.kind[1].srs == 72 &&
-           P.kind[2].rs == 512 && P.kind[2].srs == 40 && P.kind[3].rs == 1536 && P.kind[3].srs == 104;
+// the plan's phases are shape sh's (dense 4-bit rows and scale rows, o waiting for q alone)
+static bool is_shape(const ChainPlan& P, int sh) {
+    const ChainShape& S = CHAIN_SHAPES[sh];
+    if (P.combo != S.combo || P.kv_wait || P.kind[2].gu_pair != S.gu_pair || P.kind[3].fold_c != S.fold_c) return false;
+    for (int k = 0; k < 4; ++k)
+        if (P.kind[k].K != S.K[k] || P.kind[k].P != S.P[k] || P.kind[k].N != S.N[k] || P.kind[k].rs != S.rs[k] ||
+            P.kind[k].srs != S.srs[k])
+            return false;
+    return true;
 }
 
-// the kernel for a plan: the format; the poll limit a constant (FIXED) or the plan's; the C4
-// copy where the shape is Qwen3-0.6B's (and OTPU_GENERIC_COPIES was not set); the norm factors
+// the kernel for a plan: the format; the poll limit a constant (FIXED) or the plan's; a shape's
+// own copy (Qwen3-0.6B's or Qwen3-1.7B's, unless OTPU_GENERIC_COPIES was set); the norm factors
 // none / some / both in every layer; the phases' pieces a lane (combo)
+template <int FMT, int SH, int LQ, int LF>
+static const void* chain_pick_norms(int norms) {
+    return norms == 0 ? (const void*)chain_kernel<FMT, true, SH, 0, LQ, 1, LF>
+         : norms == 2 ? (const void*)chain_kernel<FMT, true, SH, 2, LQ, 1, LF>
+                      : (const void*)chain_kernel<FMT, true, SH, 1, LQ, 1, LF>;
+}
 template <int FMT>
 static const void* chain_pick_fmt(const ChainPlan& P) {
     const bool fixed = P.spin == CHAIN_SPIN;
     if (!fixed)
-        return P.combo == 1 ? (const void*)chain_kernel<FMT, false, false, 1, 2, 1, 4>
-                            : (const void*)chain_kernel<FMT, false, false, 1, 1, 1, DN_L>;
+        return P.combo == 1 ? (const void*)chain_kernel<FMT, false, 0, 1, 2, 1, 4>
+                            : (const void*)chain_kernel<FMT, false, 0, 1, 1, 1, DN_L>;
+    const bool own = OTPU_CHAIN_C4 && !P.generic;
     if (P.combo == 1)
-        return P.norms == 0 ? (const void*)chain_kernel<FMT, true, false, 0, 2, 1, 4>
-             : P.norms == 2 ? (const void*)chain_kernel<FMT, true, false, 2, 2, 1, 4>
-                            : (const void*)chain_kernel<FMT, true, false, 1, 2, 1, 4>;
-    if (OTPU_CHAIN_C4 && !P.generic && is_c4_shape(P))
-        return P.norms == 0 ? (const void*)chain_kernel<FMT, true, true, 0, 1, 1, DN_L>
-             : P.norms == 2 ? (const void*)chain_kernel<FMT, true, true, 2, 1, 1, DN_L>
-                            : (const void*)chain_kernel<FMT, true, true, 1, 1, 1, DN_L>;
-    return P.norms == 0 ? (const void*)chain_kernel<FMT, true, false, 0, 1, 1, DN_L>
-         : P.norms == 2 ? (const void*)chain_kernel<FMT, true, false, 2, 1, 1, DN_L>
-                        : (const void*)chain_kernel<FMT, true, false, 1, 1, 1, DN_L>;
+        return own && is_shape(P, 2) ? chain_pick_norms<FMT, 2, 2, 4>(P.norms) : chain_pick_norms<FMT, 0, 2, 4>(P.norms);
+    return own && is_shape(P, 1) ? chain_pick_norms<FMT, 1, 1, DN_L>(P.norms) : chain_pick_norms<FMT, 0, 1, DN_L>(P.norms);
 }
 static const void* chain_pick(const ChainPlan& P) {
     return P.fmt == OTPU_INT4 ? chain_pick_fmt<OTPU_INT4>(P) : chain_pick_fmt<OTPU_FP4>(P);

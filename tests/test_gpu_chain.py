@@ -390,13 +390,14 @@ def test_chain_c4_layers_against_the_float64_emulation(X):
                                                             ("fp4", 1024, 2048, 1024, 3072, 2),
                                                             ("int4", 2048, 2048, 1024, 6144, 2),
                                                             ("fp4", 1536, 2048, 512, 8192, 2)])
-def test_chain_persistent_formats_and_shapes(X, fmt, hidden, q_dim, kv_dim, F, layers):
+def test_chain_persistent_formats_and_shapes(X, monkeypatch, fmt, hidden, q_dim, kv_dim, F, layers):
     """The persistent step (otpu_chain_step) on fp4x6 and int4x weights, at a shape whose phases
     leave most workgroups without rows, at the largest F of the one-piece teams' copy with
-    256-column down chunks (3840), at the Qwen3-0.6B shape in fp4x6 (its shape-specialized copy;
-    int4x is the c4 test's), and in the wider teams' copy at the Qwen3-1.7B shape (hidden 2048,
-    F 6144) and at F 8192 (its largest), with per-layer norms: the oracle's step bit for bit,
-    eager and over graph replays with new inputs, the error word 0."""
+    256-column down chunks (3840), at the Qwen3-0.6B shape in fp4x6 (its shape's own copy; int4x
+    is the c4 test's), and in the wider teams' copies at the Qwen3-1.7B shape (hidden 2048,
+    F 6144: its own copy) and at F 8192 (its largest), with per-layer norms: the oracle's step
+    bit for bit, eager and over graph replays with new inputs, the error word 0; then one step
+    on the generic copy (OTPU_GENERIC_COPIES), the same bits."""
     import torch
     from opentpu_amd.chain import DecodeChain, Shape
     sh = Shape(hidden=hidden, q_dim=q_dim, kv_dim=kv_dim, F=F, layers=layers)
@@ -419,6 +420,11 @@ def test_chain_persistent_formats_and_shapes(X, fmt, hidden, q_dim, kv_dim, F, l
         assert same_bits(ch.replay(xs[i % 3]).cpu().numpy(), wants[i % 3]), f"replay {i}"
         torch.cuda.synchronize()
     assert same_bits(ch.step(xs[2]).cpu().numpy(), wants[2])
+    assert ch.chain_error() == 0
+    say("chain persistent: the generic copy")
+    monkeypatch.setenv("OTPU_GENERIC_COPIES", "1")
+    ch._plan = None                                # (a plan reads the setting when it is built)
+    assert same_bits(ch.step(xs[1]).cpu().numpy(), wants[1])
     assert ch.chain_error() == 0
 
 
