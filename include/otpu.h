@@ -198,7 +198,7 @@ int otpu_acc_rows(const float* parts, int R, int64_t pstride, int n, const float
  *   device, entries may be NULL) or NULL; x: the step's input row [hidden]; outs: the phases' fp32
  *   output rows (qkv [q_dim + 2 kv_dim], o [hidden], gu [2 F], down [hidden]); down_width: the
  *   down projection's QACT range (a multiple of 256 dividing F; the reference's chunk rule gives
- *   256 at F = 3072, 768 at F = 6144).  int4x or fp4x6 weights; hidden <= 2048, q_dim <= 2048, F
+ *   256 at F = 3072, 768 at F = 6144).  int4x, fp4x6 or nvfp4 weights; hidden <= 2048, q_dim <= 2048, F
  *   a multiple of 256 and <= 8192 (hidden <= 1024 and F <= 4096, Qwen3-0.6B's sizes, run teams of
  *   one and two pieces a lane, larger shapes up to Qwen3-1.7B's two and four), hidden and q_dim
  *   multiples of 32.

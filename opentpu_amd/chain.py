@@ -61,7 +61,7 @@ class Shape:
 class DecodeChain:
     """`layers`: per layer a dict name -> (rows, srows) device tensors (uint8).
 
-    persistent (default where it applies: fused and folded, int4 / fp4 weights, hidden <= 2048,
+    persistent (default where it applies: fused and folded, int4 / fp4 / nvfp4 weights, hidden <= 2048,
     q_dim <= 2048, F <= 8192): the whole step is one launch of otpu_chain_step, its phases handing
     rows to each other on the GPU; the same bits as the four kernels a layer below.
     fused: a layer is four kernels, each linear an otpu_mm_qin (the QACT of its input
@@ -222,8 +222,8 @@ class DecodeChain:
         # o waits for k and v as well when the q/k/v rows (32 a workgroup) span more workgroups
         # than o's (4 a workgroup); that wait holds 2048 entries
         kv_wait = -(-(s.q_dim + 2 * s.kv_dim) // 32) > -(-s.hidden // 4)
-        return (self.fused and self.fold and self.fmt in ("int4", "fp4") and s.hidden <= 2048 and s.hidden % 32 == 0
-                and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 8192 and s.F % 256 == 0
+        return (self.fused and self.fold and self.fmt in ("int4", "fp4", "nvfp4") and s.hidden <= 2048
+                and s.hidden % 32 == 0 and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 8192 and s.F % 256 == 0
                 and not (kv_wait and 2 * s.kv_dim > 2048))
 
     def _use_persistent(self) -> bool:

@@ -289,13 +289,17 @@ static const void* chain_pick_fmt(const ChainPlan& P) {
     if (!fixed)
         return P.combo == 1 ? (const void*)chain_kernel<FMT, false, 0, 1, 2, 1, 4>
                             : (const void*)chain_kernel<FMT, false, 0, 1, 1, 1, DN_L>;
-    const bool own = OTPU_CHAIN_C4 && !P.generic;
-    if (P.combo == 1)
-        return own && is_shape(P, 2) ? chain_pick_norms<FMT, 2, 2, 4>(P.norms) : chain_pick_norms<FMT, 0, 2, 4>(P.norms);
-    return own && is_shape(P, 1) ? chain_pick_norms<FMT, 1, 1, DN_L>(P.norms) : chain_pick_norms<FMT, 0, 1, DN_L>(P.norms);
+    if constexpr (FMT != OTPU_NVFP4) {          // (nvfp4's scale rows fit no shape of the table)
+        const bool own = OTPU_CHAIN_C4 && !P.generic;
+        if (own && is_shape(P, 2)) return chain_pick_norms<FMT, 2, 2, 4>(P.norms);
+        if (own && is_shape(P, 1)) return chain_pick_norms<FMT, 1, 1, DN_L>(P.norms);
+    }
+    return P.combo == 1 ? chain_pick_norms<FMT, 0, 2, 4>(P.norms) : chain_pick_norms<FMT, 0, 1, DN_L>(P.norms);
 }
 static const void* chain_pick(const ChainPlan& P) {
-    return P.fmt == OTPU_INT4 ? chain_pick_fmt<OTPU_INT4>(P) : chain_pick_fmt<OTPU_FP4>(P);
+    return P.fmt == OTPU_INT4 ? chain_pick_fmt<OTPU_INT4>(P)
+         : P.fmt == OTPU_FP4  ? chain_pick_fmt<OTPU_FP4>(P)
+                              : chain_pick_fmt<OTPU_NVFP4>(P);
 }
 
 static int64_t rnd256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -359,7 +363,8 @@ extern "C" int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, in
                                const uint8_t* const* w, const int64_t* rs, const uint8_t* const* ws,
                                const int64_t* srs, const float* rnorm, const float* const* cscale, const float* x,
                                float* const* outs, void* plan, int64_t plan_bytes) {
-    if (fmt != OTPU_INT4 && fmt != OTPU_FP4) return otpu_fail(OTPU_EINVAL, "chain_plan: int4x or fp4x6 weights");
+    if (fmt != OTPU_INT4 && fmt != OTPU_FP4 && fmt != OTPU_NVFP4)
+        return otpu_fail(OTPU_EINVAL, "chain_plan: int4x, fp4x6 or nvfp4 weights");
     if (layers < 1 || !w || !rs || !ws || !srs || !x || !outs || !plan)
         return otpu_fail(OTPU_EINVAL, "chain_plan: layers %d, NULL arrays", layers);
     // the compiled teams: combo 0 (pieces a lane 1, 1, 2) or 1 (2, 1, 4)

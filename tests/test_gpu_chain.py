@@ -389,13 +389,16 @@ def test_chain_c4_layers_against_the_float64_emulation(X):
                                                             ("int4", 1024, 2048, 512, 3840, 2),
                                                             ("fp4", 1024, 2048, 1024, 3072, 2),
                                                             ("int4", 2048, 2048, 1024, 6144, 2),
-                                                            ("fp4", 1536, 2048, 512, 8192, 2)])
+                                                            ("fp4", 1536, 2048, 512, 8192, 2),
+                                                            ("nvfp4", 1024, 2048, 1024, 3072, 2),
+                                                            ("nvfp4", 2048, 2048, 1024, 6144, 2)])
 def test_chain_persistent_formats_and_shapes(X, monkeypatch, fmt, hidden, q_dim, kv_dim, F, layers):
     """The persistent step (otpu_chain_step) on fp4x6 and int4x weights, at a shape whose phases
     leave most workgroups without rows, at the largest F of the one-piece teams' copy with
     256-column down chunks (3840), at the Qwen3-0.6B shape in fp4x6 (its shape's own copy; int4x
     is the c4 test's), and in the wider teams' copies at the Qwen3-1.7B shape (hidden 2048,
-    F 6144: its own copy) and at F 8192 (its largest), with per-layer norms: the oracle's step
+    F 6144: its own copy) and at F 8192 (its largest), nvfp4 weights at both Qwen3 shapes (the
+    generic copies: nvfp4's scale rows match no shape copy), with per-layer norms: the oracle's step
     bit for bit, eager and over graph replays with new inputs, the error word 0; then one step
     on the generic copy (OTPU_GENERIC_COPIES), the same bits."""
     import torch
