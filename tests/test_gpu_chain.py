@@ -431,6 +431,48 @@ def test_chain_persistent_formats_and_shapes(X, monkeypatch, fmt, hidden, q_dim,
     assert ch.chain_error() == 0
 
 
+@pytest.mark.parametrize("fmt,hidden,q_dim,kv_dim,F,std", [("int4", 2048, 2048, 1024, 6144, 0.03),
+                                                             ("fp4", 2048, 2048, 1024, 6144, 0.03),
+                                                             ("nvfp4", 1024, 2048, 1024, 3072, 0.04)])
+def test_chain_full_depth_persistent_equals_launches(X, fmt, hidden, q_dim, kv_dim, F, std):
+    """28 layers at the Qwen3-1.7B shape (its own copy of the persistent kernel, int4x and fp4x6)
+    and in nvfp4 at the Qwen3-0.6B shape (the generic copy): every row the persistent step leaves
+    (the last layer's q/k/v, o, gate/up products and output) equals the launch-per-linear path's
+    bit for bit (whose kernels the oracle checks: test_mm_qin_fold, the c4 test's layers), eager
+    and over graph replays; the output row is live (mostly nonzero)."""
+    import torch
+    from opentpu_amd.chain import DecodeChain, Shape
+    sh = Shape(hidden=hidden, q_dim=q_dim, kv_dim=kv_dim, F=F)
+    say("chain full depth", fmt, hidden, q_dim, kv_dim, F)
+    ch = DecodeChain.synthetic(sh, fmt, seed0=300, std=std)
+    assert ch.persistent and ch.kernels_per_step == 1
+    rng = np.random.default_rng(5)
+    xs = [rng.standard_normal((1, hidden)).astype(np.float32) for _ in range(2)]
+
+    def rows():
+        return [t.cpu().numpy().copy() for t in (ch.qkv, ch.o, ch.gu, ch.y)]
+    ch.persistent = False
+    wants = []
+    for x in xs:
+        ch.step(x)
+        wants.append(rows())
+    say("nonzero outputs", [int(np.count_nonzero(w[3])) for w in wants])
+    assert all(np.count_nonzero(w[3]) > hidden // 2 for w in wants)
+    ch.persistent = True
+    for x, want in zip(xs, wants):
+        ch.step(x)
+        for g, w in zip(rows(), want):
+            assert same_bits(g, w)
+    assert ch.chain_error() == 0
+    ch.capture()
+    for i in range(3):
+        ch.replay(xs[i % 2])
+        torch.cuda.synchronize()
+        for g, w in zip(rows(), wants[i % 2]):
+            assert same_bits(g, w), f"replay {i}"
+    assert ch.chain_error() == 0
+
+
 def test_chain_plan_refusals(X):
     """otpu_chain_plan refuses what its compiled phases cannot hold, before touching the plan."""
     import ctypes as C
