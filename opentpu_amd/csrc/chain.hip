@@ -84,7 +84,7 @@ struct ChainPlan {                               // device memory: the header, t
     int norms;                                   // 0 no RSCALE / CSCALE factors, 1 some, 2 both in every layer
     int spin;                                    // polls a wait allows
     int combo;                                   // the phases' pieces a lane: 0 (LQ, LO, LF) = (1, 1, 2), 1 (2, 1, 4)
-    int generic;                                 // never the C4 copy (OTPU_GENERIC_COPIES at plan time)
+    int generic;                                 // never a shape's own copy (OTPU_GENERIC_COPIES at plan time)
     uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
 };
 
@@ -101,9 +101,9 @@ union ChainLds {
 // FIXED: the default poll limit as a constant (folded into the waits: a limit read from the plan
 // measured 16 us a step slower); the other copy serves plans with an OTPU_CHAIN_SPIN override.
 // SH: a copy for one layer shape, its phases' K, pieces, rows and strides as constants (0: the
-// generic copy, which reads them from the plan; OTPU_CHAIN_C4=0 builds no shape copies)
-#ifndef OTPU_CHAIN_C4
-#define OTPU_CHAIN_C4 1
+// generic copy, which reads them from the plan; OTPU_CHAIN_SHAPES=0 picks no shape copies)
+#ifndef OTPU_CHAIN_SHAPES
+#define OTPU_CHAIN_SHAPES 1
 #endif
 struct ChainShape {
     int K[4], P[4], N[4], rs[4], srs[4];         // per phase: qkv, o, gu, down
@@ -254,9 +254,9 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
 }
 
 // One kernel per compiled copy of the step, each its own function: as copies of one kernel, the
-// code of each moved whenever another was added (the C4 copy measured 358 -> 363 us a step with
-// an unused copy compiled in beside it).  otpu_chain_plan picks the kernel (chain_pick) and
-// otpu_chain_step launches it.
+// code of each moved whenever another was added (the Qwen3-0.6B copy measured 358 -> 363 us a
+// step with an unused copy compiled in beside it).  otpu_chain_plan picks the kernel
+// (chain_pick) and otpu_chain_step launches it.
 template <int FMT, bool FIXED, int SH, int NORMS, int LQ, int LO, int LF>
 __global__ __launch_bounds__(256) void chain_kernel(const ChainPlan* plan) {
     __shared__ __align__(16) ChainLds lds;
@@ -290,7 +290,7 @@ static const void* chain_pick_fmt(const ChainPlan& P) {
         return P.combo == 1 ? (const void*)chain_kernel<FMT, false, 0, 1, 2, 1, 4>
                             : (const void*)chain_kernel<FMT, false, 0, 1, 1, 1, DN_L>;
     if constexpr (FMT != OTPU_NVFP4) {          // (nvfp4's scale rows fit no shape of the table)
-        const bool own = OTPU_CHAIN_C4 && !P.generic;
+        const bool own = OTPU_CHAIN_SHAPES && !P.generic;
         if (own && is_shape(P, 2)) return chain_pick_norms<FMT, 2, 2, 4>(P.norms);
         if (own && is_shape(P, 1)) return chain_pick_norms<FMT, 1, 1, DN_L>(P.norms);
     }
