@@ -176,13 +176,23 @@ __device__ __forceinline__ void ll_store(uint64_t* p, uint32_t tag, float y) {
     __hip_atomic_store(p, ((uint64_t)tag << 32) | fbits(y), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// this thread's float4 chunks c = tid + 256 k (k < CPT, c < NC) of the entry row a.ll_in: every
-// entry is loaded at once, then the entries that do not carry a.tag_in yet are loaded again until
-// they do.  A wait that runs out of polls sets *a.err and goes on with what it has (the step's
-// output is then invalid; every wave still ends).
+// this thread's float4 chunks c = tid + 256 k (k < CPT, c < NC) of the entry row a.ll_in: once
+// the row's last entry carries a.tag_in, every entry is loaded at once, then the entries that do
+// not carry it yet are loaded again until they do.  A wait that runs out of polls sets *a.err and
+// goes on with what it has (the step's output is then invalid; every wave still ends).
 template <int CPT>
 __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[CPT]) {
     const int tid = threadIdx.x;
+    // First the row's last entry alone (every thread the same address: one request a wave),
+    // which the highest-numbered producer writes, the one that tends to finish last.  Polling
+    // the whole row from the start, 256 workgroups loaded up to 6 MB a round (the fold's
+    // 24 KB input) while the producers still streamed their weights: c4 354.4-354.7 -> 326.7-
+    // 329.3 us a step (first and last entry: 333 us; middle and last: 337.6).
+    for (int n = 0;; ++n) {
+        if ((uint32_t)(ll_load(a.ll_in + 4 * NC - 1) >> 32) == a.tag_in) break;
+        if (n >= a.spin) break;                      // (the wait below sets the error word)
+        if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
+    }
     uint64_t e[CPT][4];
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
