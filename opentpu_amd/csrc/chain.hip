@@ -177,8 +177,8 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * l + k;
             MMArgs a = cload_args(P.kind[k]);
-            // stamps: 0 phase start, 1 weights issued (the wait starts), 2 input row in, 3 QACT
-            // done, 4 rows stored
+            // stamps: 0 phase start, 1 weights issued (the wait starts), 7 the input row's last
+            // entry in, 2 the whole row in, 3 QACT done, 4 rows stored (6, 5: the QACT's barrier)
             uint64_t* const st = cload(P.stamps);
             a.stamp = st ? st + ((int64_t)i * gridDim.x + b) * 8 : nullptr;
             OTPU_STAMP(a, 0);

@@ -180,9 +180,11 @@ __device__ __forceinline__ void ll_store(uint64_t* p, uint32_t tag, float y) {
 // the row's last entry carries a.tag_in, every entry is loaded at once, then the entries that do
 // not carry it yet are loaded again until they do.  A wait that runs out of polls sets *a.err and
 // goes on with what it has (the step's output is then invalid; every wave still ends).
+// (A workgroup of 256 threads: wave w's chunks of round k are the row's entries 1024 k + 256 w +
+// [0, 256).)
 template <int CPT>
 __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[CPT]) {
-    const int tid = threadIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // First the row's last entry alone (every thread the same address: one request a wave),
     // which the highest-numbered producer writes, the one that tends to finish last.  Polling
     // the whole row from the start, 256 workgroups loaded up to 6 MB a round (the fold's
@@ -193,13 +195,21 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
         if (n >= a.spin) break;                      // (the wait below sets the error word)
         if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
     }
+    OTPU_STAMP(a, 7);
+    // Lane l loads the wave's entries 64 j + l (j < 4), so that each load instruction reads 512
+    // contiguous bytes and each line of the row is requested once a wave; the chunks are then
+    // regrouped through the wave's own LDS slot.  (Lane l loading its own chunk's 4 entries, 4
+    // instructions each touched every line of the wave's 2 KB.)
+    const int n_e = 4 * NC;
+    const uint64_t* const in = a.ll_in + 256 * wave + lane;
     uint64_t e[CPT][4];
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-        const int c = tid + 256 * k;
+    for (int k = 0; k < CPT; ++k)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) e[k][j] = c < NC ? ll_load(a.ll_in + 4 * c + j) : (uint64_t)a.tag_in << 32;
-    }
+        for (int j = 0; j < 4; ++j) {
+            const int i = 1024 * k + 256 * wave + 64 * j + lane;
+            e[k][j] = i < n_e ? ll_load(in + 1024 * k + 64 * j) : (uint64_t)a.tag_in << 32;
+        }
     for (int n = 0;; ++n) {
         bool done = true;
 #pragma unroll
@@ -208,7 +218,7 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
             for (int j = 0; j < 4; ++j)
                 if ((uint32_t)(e[k][j] >> 32) != a.tag_in) {
                     done = false;
-                    e[k][j] = ll_load(a.ll_in + 4 * (tid + 256 * k) + j);
+                    e[k][j] = ll_load(in + 1024 * k + 64 * j);
                 }
         if (done) break;
         if (n >= a.spin) {
@@ -217,10 +227,14 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
         }
         if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
     }
+    // (no barrier: a wave's LDS accesses complete in order, and no other wave touches its slot)
+    __shared__ __align__(16) float slot[4][256];
 #pragma unroll
-    for (int k = 0; k < CPT; ++k)
-        xv[k] = make_float4(bitsf((uint32_t)e[k][0]), bitsf((uint32_t)e[k][1]), bitsf((uint32_t)e[k][2]),
-                            bitsf((uint32_t)e[k][3]));
+    for (int k = 0; k < CPT; ++k) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) slot[wave][64 * j + lane] = bitsf((uint32_t)e[k][j]);
+        xv[k] = reinterpret_cast<const float4*>(slot[wave])[lane];
+    }
 }
 
 // wait for entries [from, to) of the input row as well, values unused: a phase that reads part of
