@@ -219,9 +219,9 @@ int otpu_chain_plan(int layers, int hidden, int q_dim, int kv_dim, int F, int do
                     void* plan, int64_t plan_bytes);
 int otpu_chain_step(const void* plan, otpu_stream_t stream);
 int otpu_chain_error(const void* plan, uint32_t* err);
-/* Profiling: clock stamps of every phase and workgroup into stamps [4 layers][grid][8] (uint64,
- * the 100 MHz clock: phase start, weights issued, input row in, QACT done, rows stored; NULL
- * stops).  Only a library built with the stamps (python -m opentpu_amd.build --stamps); others
+/* Profiling: clock stamps of every phase and workgroup into stamps [4 layers][grid][16]
+ * (uint64, the 100 MHz clock: phase start, weights issued, input row in, QACT done, rows stored,
+ * and the counts of polls of the hand-off waits; NULL stops).  Only a library built with the stamps (python -m opentpu_amd.build --stamps); others
  * refuse (OTPU_EINVAL).  Synchronous. */
 int otpu_chain_stamps(void* plan, uint64_t* stamps);
 

@@ -85,7 +85,7 @@ struct ChainPlan {                               // device memory: the header, t
     int spin;                                    // polls a wait allows
     int combo;                                   // the phases' pieces a lane: 0 (LQ, LO, LF) = (1, 1, 2), 1 (2, 1, 4)
     int generic;                                 // never a shape's own copy (OTPU_GENERIC_COPIES at plan time)
-    uint64_t* stamps;                            // [4 layers][grid][8] clock stamps (stamped build)
+    uint64_t* stamps;                            // [4 layers][grid][16] clock stamps (stamped build)
 };
 
 // rows of phase kind k the first iteration of workgroup b covers start at b * rows_per_wg(k)
@@ -178,9 +178,10 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
             const int i = 4 * l + k;
             MMArgs a = cload_args(P.kind[k]);
             // stamps: 0 phase start, 1 weights issued (the wait starts), 7 the input row's last
-            // entry in, 2 the whole row in, 3 QACT done, 4 rows stored (6, 5: the QACT's barrier)
+            // entry in, 2 the whole row in, 3 QACT done, 4 rows stored (6, 5: the QACT's barrier);
+            // counts: 8 the last entry's polls that missed, 9 the rounds of re-polls after it
             uint64_t* const st = cload(P.stamps);
-            a.stamp = st ? st + ((int64_t)i * gridDim.x + b) * 8 : nullptr;
+            a.stamp = st ? st + ((int64_t)i * gridDim.x + b) * 16 : nullptr;
             OTPU_STAMP(a, 0);
             // (a select on k, not S.N[k]: indexed by the loop's k, the table read became a switch, and
             // the compiler then copied the rest of the phase's code for each k)

@@ -65,9 +65,16 @@ struct MMArgs {
     do {                                                                                           \
         if ((a).stamp && threadIdx.x == 0) (a).stamp[j] = __builtin_amdgcn_s_memrealtime();        \
     } while (0)
+#define OTPU_STAMP_COUNT(a, j, n)                                                                  \
+    do {                                                                                           \
+        if ((a).stamp && threadIdx.x == 0) (a).stamp[j] = (uint64_t)(n);                           \
+    } while (0)
 #else
 #define OTPU_STAMP(a, j) \
     do {                 \
+    } while (0)
+#define OTPU_STAMP_COUNT(a, j, n) \
+    do {                          \
     } while (0)
 #endif
 

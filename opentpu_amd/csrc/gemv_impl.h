@@ -190,12 +190,14 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
     // the whole row from the start, 256 workgroups loaded up to 6 MB a round (the fold's
     // 24 KB input) while the producers still streamed their weights: c4 354.4-354.7 -> 326.7-
     // 329.3 us a step (first and last entry: 333 us; middle and last: 337.6).
-    for (int n = 0;; ++n) {
+    int n = 0;
+    for (;; ++n) {
         if ((uint32_t)(ll_load(a.ll_in + 4 * NC - 1) >> 32) == a.tag_in) break;
         if (n >= a.spin) break;                      // (the wait below sets the error word)
         if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
     }
     OTPU_STAMP(a, 7);
+    OTPU_STAMP_COUNT(a, 8, n);                           // polls of the last entry that missed
     // Lane l loads the wave's entries 64 j + l (j < 4), so that each load instruction reads 512
     // contiguous bytes and each line of the row is requested once a wave; the chunks are then
     // regrouped through the wave's own LDS slot.  (Lane l loading its own chunk's 4 entries, 4
@@ -210,7 +212,7 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
             const int i = 1024 * k + 256 * wave + 64 * j + lane;
             e[k][j] = i < n_e ? ll_load(in + 1024 * k + 64 * j) : (uint64_t)a.tag_in << 32;
         }
-    for (int n = 0;; ++n) {
+    for (n = 0;; ++n) {
         bool done = true;
 #pragma unroll
         for (int k = 0; k < CPT; ++k)
@@ -227,6 +229,7 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
         }
         if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
     }
+    OTPU_STAMP_COUNT(a, 9, n);                           // wave 0's rounds of re-polls
     // (no barrier: a wave's LDS accesses complete in order, and no other wave touches its slot)
     __shared__ __align__(16) float slot[4][256];
 #pragma unroll

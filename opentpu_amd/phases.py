@@ -4,18 +4,20 @@ layers of int4x linears) from per-workgroup clock stamps.
     python -m opentpu_amd.build --stamps      # libotpu_amd_stamps.so: the stamps compiled in
     python -m opentpu_amd.phases              # on a GPU: the table below
 
-Each workgroup's first thread stamps the 100 MHz wall clock at seven points of every phase it
+Each workgroup's first thread stamps the 100 MHz wall clock at eight points of every phase it
 has rows in: phase start (0), weights issued, i.e. its wait for the input row starts (1), the
 row's last entry carrying the phase's tag (7), every entry carrying it (2), QACT done, the
 activation pieces in registers (3), rows stored (4), and around the QACT's first barrier: wave
-0's own part done (6) and every wave's done (5).  Per linear (medians over workgroups, means over
+0's own part done (6) and every wave's done (5). Per linear (medians over workgroups, means over
 the 28 layers) the table gives the intervals 0-1, 1-2 (split into the wait for the last entry,
-1-7, and the row's load and re-polls after it, 7-2), 2-3 and 3-4; the QACT interval split into wave 0's own part (2-6), the
-wait at the barrier for the other waves, whose input rows can come in later (6-5), and what
-follows the barrier (5-3); the hand-off (the previous phase's last workgroup done -> this
-phase's median workgroup with its input in: store visibility plus polling); and the tail
-(median -> last workgroup done).  Two weight copies alternate, as in bench.py; the step is replayed from a HIP
-graph.  Measurement only: the stamped library is not the product's."""
+1-7, and the row's load and re-polls after it, 7-2), 2-3 and 3-4; the QACT interval split into
+wave 0's own part (2-6), the wait at the barrier for the other waves, whose input rows can come
+in later (6-5), and what follows the barrier (5-3); the hand-off (the previous phase's last
+workgroup done -> this phase's median workgroup with its input in: store visibility plus
+polling); and the tail (median -> last workgroup done); and the mean counts of wave 0's polls of
+the last entry that missed (8) and of its rounds of re-polls of the row after it (9). Two weight
+copies alternate, as in bench.py; the step is replayed from a HIP graph.
+Measurement only: the stamped library is not the product's."""
 from __future__ import annotations
 
 import os
@@ -43,7 +45,8 @@ def breakdown(st: np.ndarray) -> dict:
             rows[NAMES[i % 4]].append([med(0, 1), med(1, 2), med(2, 3), med(3, 4),
                                        (np.median(a[:, 2]) - prev_end) * TICK_NS / 1e3,
                                        (end - np.median(a[:, 4])) * TICK_NS / 1e3, int(ran.sum()),
-                                       med(2, 6), med(6, 5), med(5, 3), med(1, 7), med(7, 2)])
+                                       med(2, 6), med(6, 5), med(5, 3), med(1, 7), med(7, 2),
+                                       np.mean(a[:, 8]), np.mean(a[:, 9])])
         prev_end = end
     return {n: np.mean(np.array(v), axis=0) for n, v in rows.items() if v}
 
@@ -68,7 +71,7 @@ def main() -> None:
         c.capture()
     torch.cuda.synchronize()
     G = torch.cuda.get_device_properties(0).multi_processor_count
-    st = torch.zeros((4 * sh.layers, G, 8), dtype=torch.int64, device="cuda")
+    st = torch.zeros((4 * sh.layers, G, 16), dtype=torch.int64, device="cuda")
     X.call("otpu_chain_stamps", C.c_void_p(chains[0]._plan_ptr()), C.c_void_p(st.data_ptr()))
     for _ in range(3):                              # steps alternating between the two copies
         chains[1]._graph.replay()
@@ -84,10 +87,10 @@ def main() -> None:
           f"{span / (4 * sh.layers):.2f} us a phase")
     print(f"{'linear':12s} {'wgs':>4s} {'start->wait':>11s} {'wait':>6s} {'(last':>6s} {'row)':>6s} "
           f"{'QACT':>6s} {'(own':>6s} {'join':>6s} {'after)':>6s} {'rows':>6s} {'hand-off':>9s} {'tail':>6s}"
-          f"   (us; medians over workgroups, means over layers)")
+          f" {'polls':>6s} {'re-polls':>8s}   (us; medians over workgroups, means over layers; polls: means)")
     for n, m in breakdown(s).items():
         print(f"{n:12s} {m[6]:4.0f} {m[0]:11.2f} {m[1]:6.2f} {m[10]:6.2f} {m[11]:6.2f} {m[2]:6.2f} {m[7]:6.2f} "
-              f"{m[8]:6.2f} {m[9]:6.2f} {m[3]:6.2f} {m[4]:9.2f} {m[5]:6.2f}")
+              f"{m[8]:6.2f} {m[9]:6.2f} {m[3]:6.2f} {m[4]:9.2f} {m[5]:6.2f} {m[12]:6.2f} {m[13]:8.2f}")
 
 
 if __name__ == "__main__":
