@@ -169,6 +169,13 @@ __device__ __forceinline__ double xsum(double x, int o) {
 #ifndef OTPU_LL_SLEEP
 #define OTPU_LL_SLEEP 1                          // s_sleep between polls (64 clocks a unit)
 #endif
+// s_sleep between the polls of a hand-off row's last entry: ~1000 clocks, about one round trip.
+// Fewer requests on that line measured faster than an earlier sight of it: c4 313.7-314.3 us a
+// step at 1, 311.3-311.7 at 8, 309.3-311.5 at 12, 309.3-309.7 at 16, 308.9-311.0 at 24
+// (interleaved, one box); 2-4 polls in flight at once measured 319-332.
+#ifndef OTPU_LL_LAST_SLEEP
+#define OTPU_LL_LAST_SLEEP 16
+#endif
 __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -194,7 +201,7 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
     for (;; ++n) {
         if ((uint32_t)(ll_load(a.ll_in + 4 * NC - 1) >> 32) == a.tag_in) break;
         if (n >= a.spin) break;                      // (the wait below sets the error word)
-        if (OTPU_LL_SLEEP) __builtin_amdgcn_s_sleep(OTPU_LL_SLEEP);
+        __builtin_amdgcn_s_sleep(OTPU_LL_LAST_SLEEP);
     }
     OTPU_STAMP(a, 7);
     OTPU_STAMP_COUNT(a, 8, n);                           // polls of the last entry that missed
