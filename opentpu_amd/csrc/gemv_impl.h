@@ -171,8 +171,8 @@ __device__ __forceinline__ double xsum(double x, int o) {
 #endif
 // s_sleep between the polls of a hand-off row's last entry: ~1000 clocks, about one round trip.
 // Fewer requests on that line measured faster than an earlier sight of it: c4 313.7-314.3 us a
-// step at 1, 311.3-311.7 at 8, 309.3-311.5 at 12, 309.3-309.7 at 16, 308.9-311.0 at 24
-// (interleaved, one box); 2-4 polls in flight at once measured 319-332.
+// step at 1, 311.3-311.7 at 8, 309.3-311.5 at 12, 309.3-309.7 at 16, 308.9-311.0 at 24,
+// 317.0-318.9 at 32 (interleaved, one box); 2-4 polls in flight at once measured 319-332.
 #ifndef OTPU_LL_LAST_SLEEP
 #define OTPU_LL_LAST_SLEEP 16
 #endif
