@@ -191,7 +191,7 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
         for (int k = 0; k < CPT; ++k) {
             const int c = tid + 256 * k;
             if (c >= NC) continue;                           // whole waves: uniform
-            const int r0 = (c >> 6) / FC * FC;
+            const int r0 = c >> 6 < FC ? 0 : udiv_small(c >> 6, FC) * FC;
             uint32_t m = 0;
             for (int j = 0; j < FC; ++j) m = max(m, smaxs[r0 + j]);
             am[k] = m;
@@ -297,6 +297,7 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
             // range's FC of them (integers below 2^53: exact in double), then the range's
             // epilogue, and folds the ranges in order
             double acc = 0.0;
+            int in_range = 0;                            // sub-ranges of the current range so far
 #pragma unroll
             for (int i = 0; i < L; ++i) {
                 float vh[GPT], vl[GPT], vs[GPT];
@@ -308,7 +309,8 @@ __device__ __forceinline__ void fold_body(const MMArgs& a, FoldLds* lds = nullpt
                     const int u = i * GPT + g;
                     if (u >= NS) continue;
                     acc += __hiloint2double(__float_as_int(vh[g]), __float_as_int(vl[g]));
-                    if ((u + 1) % FC == 0) {
+                    if (++in_range == FC) {              // (a count, not (u + 1) % FC: no division)
+                        in_range = 0;
                         const float yv = fmul_f(fmul_f((float)acc, swf), vs[g]);
                         y = u + 1 > FC ? fadd_f(y, yv) : yv;
                         acc = 0.0;

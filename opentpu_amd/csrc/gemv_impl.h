@@ -191,7 +191,9 @@ __device__ __forceinline__ void ll_store(uint64_t* p, uint32_t tag, float y) {
 // [0, 256).)
 template <int CPT>
 __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[CPT]) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // (the mask tells the compiler that wave < 4, so that where NC is a constant the bounds
+    // below resolve at compile time)
+    const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
     // First the row's last entry alone (every thread the same address: one request a wave),
     // which the highest-numbered producer writes, the one that tends to finish last.  Polling
     // the whole row from the start, 256 workgroups loaded up to 6 MB a round (the fold's
@@ -210,15 +212,23 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
     // regrouped through the wave's own LDS slot.  (Lane l loading its own chunk's 4 entries, 4
     // instructions each touched every line of the wave's 2 KB.)
     const int n_e = 4 * NC;
-    const uint64_t* const in = a.ll_in + 256 * wave + lane;
+    // Entries past the row: a round wholly past it loads nothing and reads as carrying the tag
+    // (a uniform test); in a round that ends inside the wave's part the lanes past the row load
+    // the row's last entry instead of branching round their loads (a select on the loaded value
+    // here would wait for each load before the next), and their values read as 0 at the regroup.
     uint64_t e[CPT][4];
 #pragma unroll
     for (int k = 0; k < CPT; ++k)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = 1024 * k + 256 * wave + 64 * j + lane;
-            e[k][j] = i < n_e ? ll_load(in + 1024 * k + 64 * j) : (uint64_t)a.tag_in << 32;
-        }
+        for (int j = 0; j < 4; ++j) e[k][j] = (uint64_t)a.tag_in << 32;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k)
+        if (1024 * k + 256 * wave < n_e)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 1024 * k + 256 * wave + 64 * j + lane;
+                e[k][j] = ll_load(a.ll_in + (i < n_e ? i : n_e - 1));
+            }
     for (n = 0;; ++n) {
         bool done = true;
 #pragma unroll
@@ -227,7 +237,8 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
             for (int j = 0; j < 4; ++j)
                 if ((uint32_t)(e[k][j] >> 32) != a.tag_in) {
                     done = false;
-                    e[k][j] = ll_load(in + 1024 * k + 64 * j);
+                    const int i = 1024 * k + 256 * wave + 64 * j + lane;
+                    e[k][j] = ll_load(a.ll_in + (i < n_e ? i : n_e - 1));
                 }
         if (done) break;
         if (n >= a.spin) {
@@ -242,7 +253,8 @@ __device__ __forceinline__ void ll_chunks(const MMArgs& a, int NC, float4 (&xv)[
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) slot[wave][64 * j + lane] = bitsf((uint32_t)e[k][j]);
+        for (int j = 0; j < 4; ++j)
+            slot[wave][64 * j + lane] = 1024 * k + 256 * wave + 64 * j + lane < n_e ? bitsf((uint32_t)e[k][j]) : 0.0f;
         xv[k] = reinterpret_cast<const float4*>(slot[wave])[lane];
     }
 }

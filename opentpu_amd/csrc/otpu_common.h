@@ -102,6 +102,16 @@ __device__ __forceinline__ int q8(float x) {
     return min(max(r, -127), 127);
 }
 
+// floor(x / d) for 0 <= x < 2^16 and 1 <= d < 2^16, without the integer division's long
+// sequence: the float quotient from the reciprocal (within 1 ulp) is off by at most one, which
+// the two corrections remove
+__device__ __forceinline__ int udiv_small(int x, int d) {
+    int q = (int)((float)x * __builtin_amdgcn_rcpf((float)d));
+    if ((q + 1) * d <= x) ++q;
+    if (q * d > x) --q;
+    return q;
+}
+
 __device__ __forceinline__ int window_of(int fmt) {
     return fmt == OTPU_INT8 ? 16 : (fmt == OTPU_NVFP4 ? 13 : 11);
 }
