@@ -48,10 +48,14 @@ constexpr int CHAIN_SPIN = 1 << 16;             // polls a wait allows (~1 us ea
 constexpr int CHAIN_PAD_LDS = 96 * 1024;        // dynamic LDS that keeps one workgroup a CU
 
 // the phases' teams: T lanes a row, R rows a team (the prologue QACT holds K <= 32 T elements)
+// q/k/v: 2 rows a team, so that 4096 rows (Qwen3-0.6B's and 1.7B's q, k and v) take the 256
+// workgroups of one a CU with one row group each (4 rows a team: 128 workgroups of 32 rows, the
+// other half of the chip idle in the phase, its rows 0.60 us; c4 297.3-298.4 -> 289.4-290.5 us a
+// step, the Qwen3-1.7B shape 540-545 -> 523-526, interleaved on one box)
 #ifndef OTPU_CHAIN_R
-#define OTPU_CHAIN_R 4
+#define OTPU_CHAIN_R 2
 #endif
-constexpr int QKV_T = 32, QKV_R = OTPU_CHAIN_R; // (the gate/up phase's body too when R is 4: one copy)
+constexpr int QKV_T = 32, QKV_R = OTPU_CHAIN_R;
 #ifndef OTPU_CHAIN_OR
 #define OTPU_CHAIN_OR 1
 #endif
@@ -230,7 +234,7 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
                 const uint8_t* const next = cload(LY[l + 1 < NL ? l + 1 : l].w[0]);
                 fold_body<FMT, LF, DN_T, true>(a, &lds.f);
                 asm volatile("" ::"s"(next));
-            } else if (SH != 0 && (k == 0 || k == 2)) { // q/k/v and gate/up: one call site, one body
+            } else if (SH != 0 && (k == 0 || k == 2)) { // q/k/v and gate/up: their shape constants (one body when their teams match)
                 if constexpr (SH != 0) {
                     static_assert(S.K[0] == S.K[2] && S.P[0] == S.P[2] && S.rs[0] == S.rs[2] && S.srs[0] == S.srs[2],
                                   "q/k/v and gate/up share their K");
@@ -238,7 +242,8 @@ __device__ __forceinline__ void chain_run(const ChainPlan& P, ChainLds& lds) {
                     a.N = k == 0 ? S.N[0] : S.N[2];
                     a.gu_pair = k == 0 ? 0 : S.gu_pair;
                 }
-                if (i == 0) gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, false, NRM>(a, &lds.q);   // plain x0
+                if (i == 0) gemv_body<FMT, 1, LQ, QKV_T, false, true, QKV_R, true, false, NRM>(a, &lds.q);   // plain x0
+                else if (QKV_R != GU_R && k == 0) gemv_body<FMT, 1, LQ, QKV_T, false, true, QKV_R, true, true, NRM>(a, &lds.q);
                 else gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
             } else if (k == 2) {
                 gemv_body<FMT, 1, LQ, GU_T, false, true, GU_R, true, true, NRM>(a, &lds.q);
