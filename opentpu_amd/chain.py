@@ -219,9 +219,11 @@ class DecodeChain:
     def persistent_fits(self) -> bool:
         """Whether otpu_chain_step can run this chain (its phases' teams are compiled in)."""
         s = self.shape
-        # o waits for k and v as well when the q/k/v rows (32 a workgroup) span more workgroups
-        # than o's (4 a workgroup); that wait holds 2048 entries
-        kv_wait = -(-(s.q_dim + 2 * s.kv_dim) // 32) > -(-s.hidden // 4)
+        # o waits for k and v as well when the q/k/v rows (16 a workgroup) span more workgroups
+        # than o's (4 a workgroup); that wait holds 2048 entries.  (The plan caps both counts at
+        # the CUs; without the cap this test flags a superset, so a chain it passes is never
+        # refused.)
+        kv_wait = -(-(s.q_dim + 2 * s.kv_dim) // 16) > -(-s.hidden // 4)
         return (self.fused and self.fold and self.fmt in ("int4", "fp4", "nvfp4") and s.hidden <= 2048
                 and s.hidden % 32 == 0 and s.q_dim <= 2048 and s.q_dim % 32 == 0 and s.F <= 8192 and s.F % 256 == 0
                 and not (kv_wait and 2 * s.kv_dim > 2048))

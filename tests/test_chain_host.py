@@ -56,3 +56,23 @@ def test_no_check_inside_a_capture(chain, monkeypatch):
     monkeypatch.setattr(CH.DecodeChain, "chain_error", lambda self: 1)
     monkeypatch.setattr(_Cuda, "capturing", True)
     assert chain.step() == "y"                            # no sync may be issued while capturing
+
+
+def _fits(hidden, q_dim, kv_dim, F, fmt="int4"):
+    ch = CH.DecodeChain.__new__(CH.DecodeChain)
+    ch.shape = CH.Shape(hidden=hidden, q_dim=q_dim, kv_dim=kv_dim, F=F)
+    ch.fused, ch.fold, ch.fmt = True, True, fmt
+    return ch.persistent_fits()
+
+
+def test_persistent_fits_the_plan_rules():
+    """Which chains take the persistent step: the Qwen3 shapes; a shape whose q/k/v rows span
+    more workgroups than o's (o then also waits for k and v) while that wait's 2 kv_dim entries
+    fit in 2048 (the GPU test runs it); not when they do not, and not past the compiled teams."""
+    assert _fits(1024, 2048, 1024, 3072)                  # Qwen3-0.6B
+    assert _fits(2048, 2048, 1024, 6144)                  # Qwen3-1.7B
+    assert _fits(256, 512, 512, 768)                      # q/k/v on 96 workgroups, o on 64
+    assert not _fits(256, 512, 1536, 768)                 # the same, with 3072 k and v entries
+    assert not _fits(4096, 4096, 1024, 12288)             # hidden past 2048
+    assert not _fits(1024, 2048, 1024, 3072, "int8")      # 4-bit weights only
+    assert not _fits(1024, 2048, 1024, 3000)              # F a multiple of 256

@@ -384,7 +384,8 @@ def test_chain_c4_layers_against_the_float64_emulation(X):
             assert err <= EMU_TOL * np.abs(me[k]).max(), (l, k, err / np.abs(me[k]).max())
 
 
-@pytest.mark.parametrize("fmt,hidden,q_dim,kv_dim,F,layers", [("fp4", 512, 1024, 256, 1536, 4),
+@pytest.mark.parametrize("fmt,hidden,q_dim,kv_dim,F,layers", [("int4", 256, 512, 512, 768, 2),
+                                                            ("fp4", 512, 1024, 256, 1536, 4),
                                                             ("int4", 512, 1024, 256, 1536, 4),
                                                             ("int4", 1024, 2048, 512, 3840, 2),
                                                             ("fp4", 1024, 2048, 1024, 3072, 2),
@@ -393,8 +394,9 @@ def test_chain_c4_layers_against_the_float64_emulation(X):
                                                             ("nvfp4", 1024, 2048, 1024, 3072, 2),
                                                             ("nvfp4", 2048, 2048, 1024, 6144, 2)])
 def test_chain_persistent_formats_and_shapes(X, monkeypatch, fmt, hidden, q_dim, kv_dim, F, layers):
-    """The persistent step (otpu_chain_step) on fp4x6 and int4x weights, at a shape whose phases
-    leave most workgroups without rows, at the largest F of the one-piece teams' copy with
+    """The persistent step (otpu_chain_step) on fp4x6 and int4x weights, at a shape whose q/k/v
+    rows span more workgroups than o's (96 against 64: o then waits for the k and v entries as
+    well), at a shape whose phases leave most workgroups without rows, at the largest F of the one-piece teams' copy with
     256-column down chunks (3840), at the Qwen3-0.6B shape in fp4x6 (its shape's own copy; int4x
     is the c4 test's), and in the wider teams' copies at the Qwen3-1.7B shape (hidden 2048,
     F 6144: its own copy) and at F 8192 (its largest), nvfp4 weights at both Qwen3 shapes (the
