@@ -1,5 +1,5 @@
-"""The reference-side binding INTEGRATION.md shows (the ctypes module a maintainer would add to
-openTPU), run as written with the library path filled in: its argument lists against
+"""The reference-side binding the repository's integration guide shows (the ctypes module a
+maintainer would add to openTPU), run as written with the library path filled in: its argument lists against
 include/otpu.h's prototypes and its ABI check (CPU), then its quantize_mx and mm against the
 oracle bit for bit (GPU; `opentpu/fp32.py:321-343`, `opentpu/isasim.py:749-910`)."""
 import os
@@ -24,7 +24,7 @@ def example_source():
 
 def load_example():
     ns = {"__name__": "hip_mxu_example"}
-    exec(compile(example_source(), "INTEGRATION.md (binding example)", "exec"), ns)
+    exec(compile(example_source(), "the integration guide's binding example", "exec"), ns)
     return ns
 
 
