@@ -1,7 +1,7 @@
 """The reference-side binding the repository's integration guide shows (the ctypes module a
-maintainer would add to openTPU), run as written with the library path filled in: its argument lists against
-include/otpu.h's prototypes and its ABI check (CPU), then its quantize_mx and mm against the
-oracle bit for bit (GPU; `opentpu/fp32.py:321-343`, `opentpu/isasim.py:749-910`)."""
+maintainer would add to openTPU), run as written with the library path filled in: its argument
+lists against include/otpu.h's prototypes and its ABI check (CPU), then its quantize_mx and mm
+against the oracle bit for bit (GPU; `opentpu/fp32.py:321-343`, `opentpu/isasim.py:749-910`)."""
 import os
 import re
 
